@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of the MoE layer of Qwen3.6-35B-A3B on one MI355X (synthetic GGUF Q4_K/Q6_K weights).
+
+Workload of the headline number: decode at batch 1 through 40 stacked layers of the full shape (hidden 2048,
+256 experts of width 512, top-8, shared expert of width 512; gate/up Q4_K, down Q6_K, fp32 router), all 40
+layers' experts resident in HBM (21 GB), a different input vector per layer and step so the routed experts
+change (and the 256 MB Infinity Cache cannot serve repeats). One step = one token through the 40 layers, captured
+once as a HIP graph per input set and replayed.
+  value = microseconds per token per layer (lower is better); hbm_gbps = algorithmic bytes / that time.
+Also reported (same JSON line): batched decode at 64 tokens with Zipf(1.1)-shaped routing, and a 4096-token
+prefill chunk, each through the 40 layers; the per-stage kernel times of the layer (HIP events, live); and the CPU
+oracle (numpy dequantize + fp32 matmul) timed on a bounded sample on this host.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "willow-v2_amd"))
+sys.path.insert(0, ROOT)
+
+HIDDEN, INTER, EXPERTS, TOP_K, LAYERS = 2048, 512, 256, 8, 40
+Q4K_ROW = HIDDEN // 256 * 144       # 1152 B: a gate/up row
+Q6K_ROW = INTER // 256 * 210        # 420 B: a down row
+GATE_UP_BYTES = 2 * INTER * Q4K_ROW  # 1,179,648 B per expert
+DOWN_BYTES = HIDDEN * Q6K_ROW        # 860,160 B per expert
+EXPERT_BYTES = GATE_UP_BYTES + DOWN_BYTES
+ROUTER_BYTES = EXPERTS * HIDDEN * 4
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+METRIC = "MoE layer µs/token + achieved HBM GB/s (decode b=1,64); prefill tok/s, MFMA %"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gen_q4k(torch, n, gen):
+    b = torch.randint(0, 256, (n, 144), dtype=torch.uint8, device="cuda", generator=gen)
+    for off in (0, 2):
+        d = (torch.randn(n, device="cuda", generator=gen).abs() * 0.01).half()
+        b[:, off:off + 2] = d.view(torch.uint8).view(n, 2)
+    return b
+
+
+def gen_q6k(torch, n, gen):
+    b = torch.randint(0, 256, (n, 210), dtype=torch.uint8, device="cuda", generator=gen)
+    sc = torch.randint(-32, 32, (n, 16), dtype=torch.int8, device="cuda", generator=gen)
+    b[:, 192:208] = sc.view(torch.uint8)
+    d = (torch.randn(n, device="cuda", generator=gen).abs() * 0.01).half()
+    b[:, 208:210] = d.view(torch.uint8).view(n, 2)
+    return b
+
+
+def build_layers(torch, hip, n_layers, zipf=False, seed=1):
+    """n_layers independent full-shape layers, generated on the GPU with the same recipes as gguf.synth (the
+    bytes differ from the numpy generator's; the distributions are the same)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        gate_up = gen_q4k(torch, EXPERTS * 2 * INTER * (HIDDEN // 256), gen).view(EXPERTS, -1)
+        down = gen_q6k(torch, EXPERTS * HIDDEN * (INTER // 256), gen).view(EXPERTS, -1)
+        router = torch.randn(EXPERTS, HIDDEN, device="cuda", generator=gen) * 0.02
+        sgu = gen_q4k(torch, 2 * INTER * (HIDDEN // 256), gen).view(-1)
+        sdn = gen_q6k(torch, HIDDEN * (INTER // 256), gen).view(-1)
+        sgate = torch.randn(HIDDEN, device="cuda", generator=gen) * 0.02
+        bias = None
+        if zipf:
+            perm = torch.randperm(EXPERTS, device="cuda", generator=gen)
+            bias = torch.empty(EXPERTS, device="cuda")
+            bias[perm] = -1.1 * torch.log(torch.arange(1, EXPERTS + 1, device="cuda", dtype=torch.float32))
+        layers.append(hip.MoELayer(gate_up=gate_up, down=down, router=router, router_bias=bias, hidden=HIDDEN,
+                                   inter=INTER, n_experts=EXPERTS, top_k=TOP_K, shared_gate_up=sgu,
+                                   shared_down=sdn, shared_gate=sgate, shared_inter=INTER))
+    return layers
+
+
+class HipEvents:
+    """hipEvent_t through ctypes on the HIP runtime torch itself loaded (so they live in torch's context)."""
+
+    def __init__(self, torch):
+        path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+        self.rt = ctypes.CDLL(path)
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        arr = (ctypes.c_void_p * n)()
+        for i in range(n):
+            h = ctypes.c_void_p()
+            assert self.rt.hipEventCreate(ctypes.byref(h)) == 0
+            arr[i] = h
+        return arr
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        assert self.rt.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, arr):
+        for h in arr:
+            self.rt.hipEventDestroy(h)
+
+
+def stage_bytes(stage, T, U, shared=True):
+    """Algorithmic HBM bytes of one stage for T tokens whose routing touches U distinct experts."""
+    P = T * TOP_K
+    S = 1 if shared else 0
+    if stage == "router":
+        return ROUTER_BYTES + HIDDEN * 4 + T * HIDDEN * 4 + T * EXPERTS * 4
+    if stage == "gate_up":
+        return (U + S) * GATE_UP_BYTES + T * HIDDEN * 4 + (P + T * S) * INTER * 4
+    if stage == "down":
+        return (U + S) * DOWN_BYTES + (P + T * S) * (INTER + HIDDEN) * 4
+    if stage == "combine":
+        return (P + T * S) * HIDDEN * 4 + T * HIDDEN * 4
+    return 0
+
+
+def layer_bytes(T, U):
+    """The touched bytes of a layer for T tokens (BASELINE's accounting: experts + router + gate + x/y)."""
+    return (U + 1) * EXPERT_BYTES + ROUTER_BYTES + HIDDEN * 4 + T * HIDDEN * 4 * 2
+
+
+def unique_experts(torch, layers, xs, T):
+    """Distinct experts per layer for each input set, from an eager run that returns the routing."""
+    counts = []
+    for xset in xs:
+        for l, layer in enumerate(layers):
+            ids = torch.empty(T, TOP_K, dtype=torch.int32, device="cuda")
+            layer(xset[l], ids=ids)
+            counts.append(ids)
+    torch.cuda.synchronize()
+    return [int(torch.unique(ids).numel()) for ids in counts]
+
+
+def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label):
+    """One step = T tokens through every layer; returns timings and byte counts."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1000 + T)
+    L = len(layers)
+    xs = [torch.randn(L, T, HIDDEN, device="cuda", generator=gen) for _ in range(n_sets)]
+    ys = torch.empty(L, T, HIDDEN, device="cuda")
+    ws = torch.empty(max(layer.workspace_bytes(T) for layer in layers), dtype=torch.uint8, device="cuda")
+    graphs = []
+    capture = torch.cuda.Stream()
+    for xset in xs:
+        for l, layer in enumerate(layers):  # warm the kernels once outside capture
+            layer(xset[l], out=ys[l], workspace=ws)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=capture):
+            for l, layer in enumerate(layers):
+                layer(xset[l], out=ys[l], workspace=ws)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        graphs[i % n_sets].replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end)
+    assert torch.isfinite(ys).all(), f"{label}: non-finite outputs"
+    U = unique_experts(torch, layers, xs, T)
+    us_layer = ms * 1000.0 / (steps * L)
+    bytes_layer = sum(layer_bytes(T, u) for u in U) / len(U)
+    log(f"{label}: {ms / steps:.3f} ms/step, {us_layer:.2f} us/layer, {us_layer / T:.3f} us/token/layer, "
+        f"{bytes_layer / us_layer / 1e3:.0f} GB/s, mean unique experts {sum(U) / len(U):.1f}")
+    del graphs
+    return {"ms_per_step": ms / steps, "wall_s": wall, "us_per_layer": us_layer, "us_per_token_layer": us_layer / T,
+            "bytes_per_layer": bytes_layer, "hbm_gbps": bytes_layer / us_layer / 1e3, "unique": U, "xs": xs,
+            "ws": ws}
+
+
+def profile_stages(torch, hip, layers, xs, T, ws, reps=2):
+    """Per-stage durations of the layer from HIP events recorded between its kernels (eager, same stream)."""
+    ev = HipEvents(torch)
+    n_st = hip.library().wl_moe_stage_count()
+    names = [hip.library().wl_moe_stage_name(i).decode() for i in range(n_st)]
+    calls = []
+    stream = torch.cuda.current_stream().cuda_stream
+    out = torch.empty(T, HIDDEN, device="cuda")
+    for _ in range(reps):
+        for xset in xs:
+            for l, layer in enumerate(layers):
+                events = ev.create(n_st + 1)
+                x = xset[l].contiguous()
+                hip.check(hip.library().wl_moe_layer_profile(ctypes.byref(layer.struct), x.data_ptr(), T,
+                                                             out.data_ptr(), None, None, ws.data_ptr(), ws.numel(),
+                                                             stream, events))
+                calls.append(events)
+    torch.cuda.synchronize()
+    per = {n: [] for n in names}
+    for events in calls:
+        for i, n in enumerate(names):
+            per[n].append(ev.elapsed_ms(events[i], events[i + 1]) * 1000.0)
+        ev.destroy(events)
+    return {n: sum(v) / len(v) for n, v in per.items()}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The CPU oracle (numpy dequantize of the touched experts + fp32 BLAS matmuls): decode of single tokens
+    through one full-shape layer, until the time budget is spent."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from gguf import synth
+    from oracle import moe_ref
+    lw = synth.moe_layer(1)
+    tokens = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        moe_ref.layer(synth.tokens(10 + tokens, 1), lw)
+        tokens += 1
+    dt = time.perf_counter() - t0
+    threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    us = dt / tokens * 1e6
+    return {"value": round(us, 1), "unit": "us/token/layer", "cores": int(threads), "kind": "port",
+            "sample": f"{tokens} decode tokens (b=1) through one full-shape layer (256 experts, top-8, shared; "
+                      f"seed-1 weights), numpy dequantize + fp32 BLAS matmul; {np.__name__} {np.__version__}",
+            "hbm_equiv_gbps": round(layer_bytes(1, 8) / us / 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--sets", type=int, default=8, help="distinct input sets (graphs) cycled through")
+    ap.add_argument("--skip-b64", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build's MoE layer runs on a single MI355X (expert-parallel "
+              "sharding across GPUs is designed, not built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from gguf import hip
+    torch.cuda.set_device(0)
+    hip.library()
+
+    log(f"building {args.layers} layers in HBM")
+    t = time.time()
+    layers = build_layers(torch, hip, args.layers)
+    torch.cuda.synchronize()
+    log(f"built in {time.time() - t:.1f}s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated")
+
+    d1 = run_decode(torch, hip, layers, 1, args.steps, args.warmup, args.sets, "decode b=1")
+    stages = profile_stages(torch, hip, layers, d1["xs"], 1, d1["ws"])
+    log("stage us (b=1): " + ", ".join(f"{k} {v:.2f}" for k, v in stages.items()))
+    U1 = sum(d1["unique"]) / len(d1["unique"])
+    dominant = max(stages, key=stages.get)
+    dom_bytes = stage_bytes(dominant, 1, U1)
+    achieved = dom_bytes / stages[dominant] / 1e3  # GB/s
+    result = {
+        "metric": METRIC,
+        "value": round(d1["us_per_token_layer"], 3),
+        "unit": "us/token/layer",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(d1["ms_per_step"], 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"decode b=1 through {args.layers} stacked Qwen3.6-35B-A3B MoE layers (hidden 2048, "
+                               "256 experts x width 512, top-8, shared expert; gate/up Q4_K, down Q6_K, fp32 "
+                               "router), all experts HBM-resident",
+                   "layers": args.layers, "tokens_per_step": 1, "input_sets": args.sets, "graph": "hipGraph"},
+        "hbm_gbps": round(d1["hbm_gbps"], 1),
+        "hbm_frac": round(d1["hbm_gbps"] / HBM_PEAK_GBPS, 4),
+        "stages_us_b1": {k: round(v, 3) for k, v in stages.items()},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": int(dom_bytes)},
+    }
+    del d1
+    if not args.skip_b64:
+        zl = build_layers(torch, hip, args.layers, zipf=True, seed=3) if True else None
+        del layers
+        torch.cuda.empty_cache()
+        d64 = run_decode(torch, hip, zl, 64, max(10, args.steps // 10), max(2, args.warmup // 4), 4, "decode b=64")
+        result["decode_b64"] = {"us_per_token_layer": round(d64["us_per_token_layer"], 3),
+                                "us_per_layer": round(d64["us_per_layer"], 2),
+                                "hbm_gbps": round(d64["hbm_gbps"], 1),
+                                "mean_unique_experts": round(sum(d64["unique"]) / len(d64["unique"]), 1),
+                                "routing": "Zipf(1.1) router bias"}
+        layers = zl
+        del d64
+    if not args.skip_prefill:
+        result["prefill"] = run_prefill(torch, hip, layers, 4096, steps=2)
+    if not args.skip_cpu:
+        log("timing the CPU oracle")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+def run_prefill(torch, hip, layers, T, steps):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    x = torch.randn(T, HIDDEN, device="cuda", generator=gen)
+    ws = torch.empty(max(layer.workspace_bytes(T) for layer in layers), dtype=torch.uint8, device="cuda")
+    y = torch.empty(T, HIDDEN, device="cuda")
+    layers[0](x, out=y, workspace=ws)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        for layer in layers:
+            layer(x, out=y, workspace=ws)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = len(layers) * T * (TOP_K + 1) * 3 * 2 * HIDDEN * INTER
+    log(f"prefill T={T}: {ms:.1f} ms per chunk of {len(layers)} layers, {T / ms * 1e3:.0f} tok/s")
+    return {"tokens": T, "ms_per_chunk": round(ms, 2), "tok_per_s": round(T / ms * 1e3, 1),
+            "tflops": round(flops / ms / 1e9, 2), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "path": "fp32 GEMV kernels (no MFMA yet)"}
+
+
+if __name__ == "__main__":
+    main()

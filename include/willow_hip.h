@@ -1,0 +1,139 @@
+/*
+ * willow_hip.h — C ABI of the MI355X (gfx950) MoE-layer library libwillow_hip.so.
+ *
+ * The library computes willow's Qwen3.6-35B-A3B mixture-of-experts layer straight from GGUF Q4_K / Q6_K blocks
+ * held in device memory: router, top-k selection, token->expert grouping, SwiGLU experts, and the weighted
+ * combine with the sigmoid-gated shared expert.
+ *
+ * Conventions (every entry point):
+ *   - All pointers are DEVICE pointers (hipMalloc'd, e.g. owned by torch tensors) unless the name ends in _host.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default stream. Work is only enqueued:
+ *     no entry point synchronizes, allocates device memory, or keeps mutable global state.
+ *   - Return value: 0 = ok; negative = WL_E* argument error detected on the host before anything was enqueued;
+ *     positive = the hipError_t reported by the launch. wl_error_string() describes either.
+ *   - Quantized weights are GGML blocks in the exact byte layout GGUF stores (type ids as in ggml):
+ *       Q4_K (12): 256 values / 144 B = d f16 | dmin f16 | 12 B packed 6-bit scales+mins | 128 B nibbles
+ *       Q6_K (14): 256 values / 210 B = ql[128] | qh[64] | int8 scales[16] | d f16
+ *     A [rows x k] matrix is rows of k/256 consecutive blocks; `row_stride` is the byte distance between rows.
+ *   - Activations are fp32, row-major [tokens x features]; accumulation is fp32.
+ */
+#ifndef WILLOW_HIP_H
+#define WILLOW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WL_TYPE_Q4_K 12
+#define WL_TYPE_Q6_K 14
+
+#define WL_DTYPE_F32 0
+#define WL_DTYPE_BF16 1
+
+#define WL_OK 0
+#define WL_EINVAL_TYPE -1      /* ggml type is not Q4_K or Q6_K */
+#define WL_EINVAL_SHAPE -2     /* k not a multiple of 256, a size <= 0, or a size past the library's limits */
+#define WL_EINVAL_NULL -3      /* a required pointer is NULL */
+#define WL_EINVAL_ALIGN -4     /* a base pointer or stride is not aligned as the kernels need */
+#define WL_EINVAL_TOPK -5      /* top_k < 1, top_k > n_experts, or top_k > WL_MAX_TOPK */
+#define WL_EINVAL_WORKSPACE -6 /* workspace NULL or smaller than wl_moe_workspace_bytes() */
+#define WL_EINVAL_DTYPE -7     /* output dtype is not WL_DTYPE_F32 / WL_DTYPE_BF16 */
+#define WL_EINVAL_COUNT -8     /* too many experts for one batched call */
+
+#define WL_MAX_TOPK 16
+#define WL_MAX_BATCH_EXPERTS 64 /* experts per wl_gemv_batch / wl_gemv_combine call */
+
+/* Human-readable text for a return code (static storage; never NULL). */
+const char* wl_error_string(int code);
+
+/* ABI version of this header: (major << 16) | minor. */
+int wl_abi_version(void);
+
+/* Bytes of one row of `k` values stored as `type`, or a negative WL_E* code.
+ * Replaces gguf/metal.py:323-325 (row_bytes). */
+int64_t wl_row_bytes(int type, int64_t k);
+
+/* out[rows x k] = dequantized w, as fp32 or bf16 (round to nearest even). Bit-exact with the CPU dequantizers.
+ * Replaces gguf/metal.py:357-363 (dequantize_gpu) and gguf/quants.py:207-227 (dequantize) for Q4_K / Q6_K. */
+int wl_dequant(int type, const void* w, int64_t rows, int64_t k, int64_t row_stride, int out_dtype, void* out,
+               void* stream);
+
+/* y[t, r] = sum_k W[r, k] * x[t, k] for t < tokens: x fp32 [tokens x k], y fp32 [tokens x rows].
+ * Replaces gguf/metal.py:327-334 (gemv) and the decode branch of GGMLWeight.linear (:401-408). */
+int wl_gemv(int type, const void* w, int64_t rows, int64_t k, int64_t row_stride, const float* x, int64_t tokens,
+            float* y, void* stream);
+
+/* For each i < n: out[positions_host[i], :] = W_i x, with W_i the [rows x k] matrix at byte offset
+ * offsets_host[i] from `base`; x fp32 [k], out fp32 [*, rows]. offsets/positions are HOST arrays (n <=
+ * WL_MAX_BATCH_EXPERTS) passed by value to the kernel. Replaces gguf/metal.py:336-343 (gemv_batch). */
+int wl_gemv_batch(int type, const void* base, int64_t rows, int64_t k, const int64_t* offsets_host,
+                  const int64_t* positions_host, int n, const float* x, float* out, void* stream);
+
+/* y[r] = sum over i < n, in order of i, of weights[perm_host[i]] * (W_i x_i)[r]; x fp32 [n x k], weights fp32 on
+ * the device, y fp32 [rows]. fp32 throughout (the Metal kernel rounds to bf16 at every step).
+ * Replaces gguf/metal.py:345-355 (gemv_combine). */
+int wl_gemv_combine(int type, const void* base, int64_t rows, int64_t k, const int64_t* offsets_host,
+                    const int64_t* perm_host, int n, const float* x, const float* weights, float* y, void* stream);
+
+/* One MoE layer's weights, all device pointers (a view into the HBM-resident expert store).
+ * Expert e's fused gate_up matrix [2*inter x hidden] (gate rows first, then up rows, as gguf/compiler.py:69-88
+ * fuses them) starts at gate_up + e * gate_up_stride; its down matrix [hidden x inter] at down + e * down_stride. */
+typedef struct WlMoeLayer {
+    const void* gate_up;         /* [n_experts] x [2*inter x hidden] of gate_up_type */
+    const void* down;            /* [n_experts] x [hidden x inter] of down_type */
+    const float* router;         /* fp32 [n_experts x hidden]  (mlp.gate.weight) */
+    const float* router_bias;    /* fp32 [n_experts] or NULL */
+    const void* shared_gate_up;  /* [2*shared_inter x hidden] of shared_gate_up_type, or NULL: no shared expert */
+    const void* shared_down;     /* [hidden x shared_inter] of shared_down_type */
+    const float* shared_gate;    /* fp32 [hidden] (mlp.shared_expert_gate.weight), or NULL: gate of 1 */
+    int64_t gate_up_stride;      /* bytes between experts' gate_up matrices */
+    int64_t down_stride;         /* bytes between experts' down matrices */
+    int32_t gate_up_type, down_type, shared_gate_up_type, shared_down_type;
+    int32_t hidden, inter, shared_inter;
+    int32_t n_experts, top_k, norm_topk_prob;
+} WlMoeLayer;
+
+/* Checks a layer description without touching device memory; 0 or a WL_E* code. */
+int wl_moe_check(const WlMoeLayer* layer);
+
+/* Bytes of device workspace wl_moe_layer needs for `tokens` tokens (0 on an invalid layer). */
+size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
+
+/* Router: logits = x W_r^T (+ bias) in a fixed floating-point order: hidden is cut into segments of 64
+ * consecutive values; each segment's partial is a chain of fused multiply-adds in ascending index starting from 0;
+ * the partials are added left to right; then the bias is added. Then softmax in fp32, top-k on the logits
+ * (largest first, ties -> lower expert id), renormalized when norm_topk_prob. ids int32 [tokens x top_k],
+ * weights fp32 [tokens x top_k],
+ * logits fp32 [tokens x n_experts] (workspace-sized, required). shared_gate_out fp32 [tokens] =
+ * sigmoid(x . shared_gate) when layer->shared_gate != NULL (else may be NULL).
+ * Replaces engines/base.py:448 (router linear) + :91-97 (route). */
+int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float* logits, int32_t* ids,
+                 float* weights, float* shared_gate_out, void* stream);
+
+/* The whole layer: y fp32 [tokens x hidden] = sum over the token's top_k experts, in ascending expert id, of
+ * weight * down(silu(gate x) * (up x)), plus sigmoid(x . shared_gate) * shared_down(silu(...) * (...)).
+ * ids/weights (optional, may be NULL) receive the routing. Replaces engines/base.py:445-490 (Engine.moe) with its
+ * dispatch (:456-467, :492-591) kept on the device: no host synchronization. */
+int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* wl_moe_layer with a hipEvent_t recorded on `stream` at every stage boundary: events_host[i] just before stage i,
+ * events_host[wl_moe_stage_count()] after the last (so wl_moe_stage_count() + 1 events, none NULL). For per-stage
+ * timing with hipEventElapsedTime; do not use under stream capture. No counterpart in the reference, whose only
+ * timers are host-side (engines/base.py:384-390). */
+int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
+                         float* weights, void* workspace, size_t workspace_bytes, void* stream,
+                         void* const* events_host);
+
+/* Number of stages wl_moe_layer runs, and their names ("router", "topk", "sort", "gate_up", "down", "combine"). */
+int wl_moe_stage_count(void);
+const char* wl_moe_stage_name(int stage);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WILLOW_HIP_H */

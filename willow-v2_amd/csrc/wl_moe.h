@@ -1,0 +1,60 @@
+// Shared definitions of the MoE-layer kernels: limits, kernel argument block, workspace layout.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/willow_hip.h"
+
+namespace wl {
+
+constexpr int kRouterSeg = 64;     // router: values per fused-multiply-add segment
+constexpr int kRouterMaxJ = 8;     // router: segments per lane (hidden <= 64 * 32 * 8)
+constexpr int kMaxEJ = 16;         // top-k: logits per lane (n_experts <= 1024)
+constexpr int kSortChunk = 256;    // grouping: tokens per bitmap chunk
+constexpr int kSortWords = kSortChunk / 32;
+constexpr int64_t kMaxTokens = 1 << 20;
+constexpr int kMoeStages = 6;  // router, topk, sort, gate_up, down, combine
+
+struct ExpertArgs {
+    const uint8_t* gate_up;
+    int64_t gate_up_stride;
+    const uint8_t* down;
+    int64_t down_stride;
+    const uint8_t* sh_gate_up;
+    const uint8_t* sh_down;
+    const float* x;
+    int T, H, inter, sh_inter, k;
+    int n_routed;  // grid slots [0, n_routed) are routed experts; slot n_routed (if launched) the shared expert
+    const int32_t* offsets;
+    const int32_t* active;
+    const int32_t* sorted;
+    float* h;
+    float* h_sh;
+    float* o;
+    float* o_sh;
+};
+
+struct Workspace {
+    float* logits;      // [T, E]
+    float* sg;          // [T]      sigmoid(shared gate)
+    int32_t* ids;       // [T, k]
+    float* wts;         // [T, k]
+    int32_t* corder;    // [T, k]   slots in ascending expert id
+    int32_t* rank;      // [T*k]    rank of a pair within its chunk and expert
+    int32_t* hist;      // [chunks, E]
+    int32_t* offsets;   // [E+1]
+    int32_t* active;    // [1+E]
+    int32_t* sorted;    // [T*k]
+    int32_t* pair_pos;  // [T*k]
+    float* h;           // [T*k, inter]   by sorted position
+    float* o;           // [T*k, hidden]  by sorted position
+    float* h_sh;        // [T, shared_inter]
+    float* o_sh;        // [T, hidden]
+    size_t bytes;
+};
+
+Workspace carve(const WlMoeLayer& L, int64_t T, void* base);
+int check_layer(const WlMoeLayer* L);
+
+}  // namespace wl

@@ -1,0 +1,806 @@
+// The MoE layer on the device: router, top-k, token->expert grouping, SwiGLU experts, weighted combine.
+// Replaces engines/base.py:445-591 (Engine.moe, batched_decode_experts, each_expert, combine_decode_experts) and
+// the Metal gemv_batch / gemv_combine launches it makes; routing never leaves the GPU (no host sync per layer).
+#include <hip/hip_runtime.h>
+
+#include "wl_common.h"
+#include "wl_host.h"
+#include "wl_moe.h"
+
+namespace wl {
+
+// ---------------------------------------------------------------------------------------------------------------
+// Router. logits[t, e] = x[t] . W[e] (+ bias[e]) in a fixed order the CPU oracle replays exactly:
+//   k is cut into segments of kRouterSeg consecutive values; each segment's partial is a chain of fused
+//   multiply-adds in ascending k starting from 0; the partials are added left to right; then the bias.
+// Decode mapping: 32 lanes per row (lane s owns segments s, s+32, ...), two rows per wavefront, TT tokens per pass.
+// The shared-expert gate is row E (weight vector shared_gate, no bias); its output is sigmoid(logit).
+template <int TT>
+__global__ __launch_bounds__(64) void k_router(const float* __restrict__ x, const float* __restrict__ w,
+                                               const float* __restrict__ bias,
+                                               const float* __restrict__ shared_gate, int T, int H, int E,
+                                               float* __restrict__ logits, float* __restrict__ sg) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 2 + (lane >> 5);
+    const int slot = lane & 31;
+    const int rows_total = E + (shared_gate ? 1 : 0);
+    const bool valid = row < rows_total;
+    const float* wr = row < E ? w + static_cast<int64_t>(row) * H : shared_gate;
+    const int nseg = H / kRouterSeg;
+    const int src_base = lane & 32;
+    for (int t0 = 0; t0 < T; t0 += TT) {
+        float p[kRouterMaxJ][TT];
+#pragma unroll
+        for (int j = 0; j < kRouterMaxJ; j++)
+#pragma unroll
+            for (int u = 0; u < TT; u++) p[j][u] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRouterMaxJ; j++) {
+            const int s = slot + 32 * j;
+            if (valid && s < nseg) {
+                const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
+#pragma unroll 4
+                for (int i = 0; i < kRouterSeg / 4; i++) {
+                    const float4 wv = wp[i];
+#pragma unroll
+                    for (int u = 0; u < TT; u++) {
+                        if (t0 + u < T) {
+                            const float4 xv = *reinterpret_cast<const float4*>(
+                                x + static_cast<int64_t>(t0 + u) * H + s * kRouterSeg + 4 * i);
+                            p[j][u] = __builtin_fmaf(xv.x, wv.x, p[j][u]);
+                            p[j][u] = __builtin_fmaf(xv.y, wv.y, p[j][u]);
+                            p[j][u] = __builtin_fmaf(xv.z, wv.z, p[j][u]);
+                            p[j][u] = __builtin_fmaf(xv.w, wv.w, p[j][u]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+            float total = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRouterMaxJ; j++) {
+                if (32 * j < nseg) {
+                    for (int sl = 0; sl < 32; sl++) {
+                        const int s = sl + 32 * j;
+                        if (s < nseg) {
+                            const float v = __shfl(p[j][u], src_base + sl);
+                            total = s == 0 ? v : __fadd_rn(total, v);
+                        }
+                    }
+                }
+            }
+            if (slot == 0 && valid && t0 + u < T) {
+                if (row < E)
+                    logits[static_cast<int64_t>(t0 + u) * E + row] = bias ? __fadd_rn(total, bias[row]) : total;
+                else
+                    sg[t0 + u] = sigmoid(total);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Top-k: one wavefront per token. Softmax over all E in fp32; selection on the logits (softmax is monotone),
+// largest first, ties to the lower expert id; weights p_r = exp(l_r - max) / sum, renormalized over the k picks
+// when requested (engines/base.py:91-97). corder[t, i] = the slot of the token's i-th smallest expert id, the
+// order the combine adds experts in.
+__global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, int T, int E, int k, int renorm,
+                                              int32_t* __restrict__ ids, float* __restrict__ wts,
+                                              int32_t* __restrict__ corder) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float* lt = logits + static_cast<int64_t>(t) * E;
+    float v[kMaxEJ];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kMaxEJ; j++) {
+        const int idx = lane + 64 * j;
+        const float lv = idx < E ? lt[idx] : -INFINITY;
+        v[j] = lv == lv ? lv : -INFINITY;  // a NaN logit ranks last, so k valid ids are always picked
+        m = fmaxf(m, v[j]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxEJ; j++)
+        if (lane + 64 * j < E) s += expf(v[j] - m);
+    s = group_sum<64>(s);
+    uint32_t taken = 0;
+    int my_id = 0;
+    float my_v = -INFINITY;
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < kMaxEJ; j++) {
+            const int idx = lane + 64 * j;
+            if (idx < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && idx < bi))) {
+                bv = v[j];
+                bi = idx;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == r) {
+            my_id = bi;
+            my_v = bv;
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    }
+    const float p = lane < k ? expf(my_v - m) / s : 0.0f;
+    float wsum = 0.0f;
+    for (int r = 0; r < k; r++) {
+        const float pr = __shfl(p, r);
+        wsum = r == 0 ? pr : wsum + pr;
+    }
+    int rank = 0;
+    for (int r = 0; r < k; r++) rank += __shfl(my_id, r) < my_id ? 1 : 0;
+    if (lane < k) {
+        ids[static_cast<int64_t>(t) * k + lane] = my_id;
+        wts[static_cast<int64_t>(t) * k + lane] = renorm ? p / wsum : p;
+        if (corder) corder[static_cast<int64_t>(t) * k + rank] = lane;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Token->expert grouping (a stable counting sort of the T*k (token, slot) pairs by expert id).
+// Within a chunk of kSortChunk tokens, bit t of row e of an LDS bitmap says token t picked expert e; a pair's rank
+// among its expert's pairs is the popcount of the bits before it, so the result is deterministic and stable
+// (pairs of one expert stay in token order). Outputs:
+//   offsets[E+1]    first sorted position of each expert's pairs; offsets[E] = T*k
+//   active[0]       number of experts with at least one pair; active[1..] those experts, ascending
+//   sorted[P]       pair id (t*k + slot) at each sorted position;  pair_pos[P] the inverse
+__device__ void block_exclusive_scan(int32_t* a, int n, int32_t* scratch, int32_t* total_out) {
+    // n <= 4 * blockDim.x; scratch: 2 * blockDim.x ints of LDS
+    const int tid = threadIdx.x, nt = blockDim.x;
+    int local[4];
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = tid * 4 + i;
+        local[i] = idx < n ? a[idx] : 0;
+        sum += local[i];
+    }
+    int32_t* buf0 = scratch;
+    int32_t* buf1 = scratch + nt;
+    buf0[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < nt; off <<= 1) {
+        const int val = buf0[tid] + (tid >= off ? buf0[tid - off] : 0);
+        __syncthreads();
+        buf1[tid] = val;
+        __syncthreads();
+        int32_t* tmp = buf0;
+        buf0 = buf1;
+        buf1 = tmp;
+    }
+    int run = buf0[tid] - sum;  // exclusive prefix of this thread's group
+    if (tid == nt - 1 && total_out) *total_out = buf0[tid];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int idx = tid * 4 + i;
+        if (idx < n) a[idx] = run;
+        run += local[i];
+    }
+    __syncthreads();
+}
+
+// Bitmaps of one chunk; returns with counts[e] filled (LDS) and `bits` holding the chunk's bitmap.
+__device__ void chunk_bitmap(const int32_t* __restrict__ ids, int t_begin, int t_end, int k, int E, uint32_t* bits,
+                             int32_t* counts) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int i = tid; i < E * kSortWords; i += nt) bits[i] = 0;
+    __syncthreads();
+    const int pairs = (t_end - t_begin) * k;
+    for (int q = tid; q < pairs; q += nt) {
+        const int t = q / k;
+        const int e = ids[static_cast<int64_t>(t_begin) * k + q];
+        if (e >= 0 && e < E) atomicOr(&bits[e * kSortWords + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += nt) {
+        int c = 0;
+#pragma unroll
+        for (int wd = 0; wd < kSortWords; wd++) c += __popc(bits[e * kSortWords + wd]);
+        counts[e] = c;
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int chunk_rank(const uint32_t* bits, int e, int t) {
+    int r = 0;
+    const int wd = t >> 5;
+    for (int i = 0; i < wd; i++) r += __popc(bits[e * kSortWords + i]);
+    r += __popc(bits[e * kSortWords + wd] & ((1u << (t & 31)) - 1u));
+    return r;
+}
+
+__device__ void write_active(const int32_t* counts, int E, int32_t* __restrict__ active, int32_t* flags,
+                             int32_t* scratch) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < E; e += nt) flags[e] = counts[e] > 0 ? 1 : 0;
+    __syncthreads();
+    int32_t* n_active = scratch + 2 * nt;
+    block_exclusive_scan(flags, E, scratch, n_active);
+    for (int e = tid; e < E; e += nt)
+        if (counts[e] > 0) active[1 + flags[e]] = e;
+    if (tid == 0) active[0] = *n_active;
+}
+
+// One chunk (T <= kSortChunk): everything in one workgroup.
+__global__ __launch_bounds__(256) void k_sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
+                                                    int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                                    int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos) {
+    extern __shared__ uint32_t smem[];
+    uint32_t* bits = smem;
+    int32_t* counts = reinterpret_cast<int32_t*>(bits + E * kSortWords);
+    int32_t* offs = counts + E;
+    int32_t* flags = offs + E;
+    int32_t* scratch = flags + E;  // 2 * 256 + 1
+    const int tid = threadIdx.x, nt = blockDim.x;
+    chunk_bitmap(ids, 0, T, k, E, bits, counts);
+    for (int e = tid; e < E; e += nt) offs[e] = counts[e];
+    __syncthreads();
+    block_exclusive_scan(offs, E, scratch, nullptr);
+    for (int e = tid; e < E; e += nt) offsets[e] = offs[e];
+    if (tid == 0) offsets[E] = T * k;
+    write_active(counts, E, active, flags, scratch);
+    for (int q = tid; q < T * k; q += nt) {
+        const int e = ids[q];
+        if (e < 0 || e >= E) continue;
+        const int pos = offs[e] + chunk_rank(bits, e, q / k);
+        sorted[pos] = q;
+        pair_pos[q] = pos;
+    }
+}
+
+// Many chunks: per-chunk ranks and counts, then one scan, then the scatter.
+__global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int T, int k, int E,
+                                                   int32_t* __restrict__ rank, int32_t* __restrict__ hist) {
+    extern __shared__ uint32_t smem[];
+    uint32_t* bits = smem;
+    int32_t* counts = reinterpret_cast<int32_t*>(bits + E * kSortWords);
+    const int c = blockIdx.x;
+    const int t_begin = c * kSortChunk;
+    const int t_end = min(T, t_begin + kSortChunk);
+    chunk_bitmap(ids, t_begin, t_end, k, E, bits, counts);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < E; e += nt) hist[static_cast<int64_t>(c) * E + e] = counts[e];
+    const int pairs = (t_end - t_begin) * k;
+    for (int q = tid; q < pairs; q += nt) {
+        const int64_t p = static_cast<int64_t>(t_begin) * k + q;
+        const int e = ids[p];
+        rank[p] = (e >= 0 && e < E) ? chunk_rank(bits, e, q / k) : 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_sort_scan(int T, int k, int E, int nchunks, int32_t* __restrict__ hist,
+                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ active) {
+    extern __shared__ uint32_t smem[];
+    int32_t* counts = reinterpret_cast<int32_t*>(smem);
+    int32_t* offs = counts + E;
+    int32_t* flags = offs + E;
+    int32_t* scratch = flags + E;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < E; e += nt) {
+        int run = 0;
+        for (int c = 0; c < nchunks; c++) {
+            const int64_t i = static_cast<int64_t>(c) * E + e;
+            const int b = hist[i];
+            hist[i] = run;
+            run += b;
+        }
+        counts[e] = run;
+        offs[e] = run;
+    }
+    __syncthreads();
+    block_exclusive_scan(offs, E, scratch, nullptr);
+    for (int e = tid; e < E; e += nt) {
+        offsets[e] = offs[e];
+        for (int c = 0; c < nchunks; c++) hist[static_cast<int64_t>(c) * E + e] += offs[e];
+    }
+    if (tid == 0) offsets[E] = T * k;
+    write_active(counts, E, active, flags, scratch);
+}
+
+__global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int T, int k, int E,
+                                                      const int32_t* __restrict__ rank,
+                                                      const int32_t* __restrict__ hist,
+                                                      int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (p >= static_cast<int64_t>(T) * k) return;
+    const int e = ids[p];
+    if (e < 0 || e >= E) return;
+    const int c = static_cast<int>(p / k) / kSortChunk;
+    const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
+    sorted[pos] = static_cast<int32_t>(p);
+    pair_pos[p] = pos;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Experts. grid.y = expert slot: slots [0, n_routed) are active experts (active[1 + slot]); slot n_routed, when
+// with_shared, is the shared expert over all T tokens. Outputs are indexed by sorted position (routed) or token
+// (shared).
+struct ExpertView {
+    const uint8_t* w;
+    int64_t stride_rows;  // offset of the up half (gate_up) in rows
+    int begin, end;       // token positions
+    bool routed;
+};
+
+__device__ __forceinline__ bool expert_view(const ExpertArgs& a, int slot, bool up_proj, ExpertView& v) {
+    if (slot < a.n_routed) {
+        if (slot >= a.active[0]) return false;
+        const int e = a.active[1 + slot];
+        v.w = (up_proj ? a.gate_up : a.down) + static_cast<int64_t>(e) * (up_proj ? a.gate_up_stride : a.down_stride);
+        v.stride_rows = a.inter;
+        v.begin = a.offsets[e];
+        v.end = a.offsets[e + 1];
+        v.routed = true;
+    } else {
+        v.w = up_proj ? a.sh_gate_up : a.sh_down;
+        v.stride_rows = a.sh_inter;
+        v.begin = 0;
+        v.end = a.T;
+        v.routed = false;
+    }
+    return true;
+}
+
+// gate_up + SwiGLU: wave = one intermediate row j (gate row j and up row inter + j); lanes split the hidden dim
+// into blocks (group g -> blocks g, g+8, ...). h[pos, j] = silu(gate . x_t) * (up . x_t).
+template <int TYPE, int TT>
+__global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a) {
+    ExpertView v;
+    if (!expert_view(a, blockIdx.y, true, v)) return;
+    const int inter = static_cast<int>(v.stride_rows);
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j >= inter) return;
+    const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
+    const int nb = a.H / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const uint8_t* wg = v.w + static_cast<int64_t>(j) * rs;
+    const uint8_t* wu = v.w + static_cast<int64_t>(inter + j) * rs;
+    const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
+    float* hout = v.routed ? a.h : a.h_sh;
+    for (int p0 = v.begin; p0 < v.end; p0 += TT) {
+        int tok[TT];
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+            const int pos = p0 + u;
+            tok[u] = pos < v.end ? (v.routed ? a.sorted[pos] / a.k : pos) : -1;
+        }
+        float ag[TT], au[TT];
+#pragma unroll
+        for (int u = 0; u < TT; u++) ag[u] = au[u] = 0.0f;
+        for (int kb = g; kb < nb; kb += 8) {
+            Lane32 lg, lu;
+            decode<TYPE>(wg + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lg);
+            decode<TYPE>(wu + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lu);
+#pragma unroll
+            for (int u = 0; u < TT; u++) {
+                if (tok[u] >= 0) {
+                    const float* xt = a.x + static_cast<int64_t>(tok[u]) * a.H + kb * kQK + lo_start;
+                    float4 xl[4], xh[4];
+                    load_run(xt, xl);
+                    load_run(xt + hi_off, xh);
+                    const float sxl = sum16(xl), sxh = sum16(xh);
+                    ag[u] += lane_dot_s(lg, xl, xh, sxl, sxh);
+                    au[u] += lane_dot_s(lu, xl, xh, sxl, sxh);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+            const float gs = group_sum<64>(ag[u]);
+            const float us = group_sum<64>(au[u]);
+            if (lane == 0 && tok[u] >= 0) {
+                const int64_t row = v.routed ? p0 + u : tok[u];
+                hout[row * inter + j] = silu(gs) * us;
+            }
+        }
+    }
+}
+
+// down: wave = R output rows (nb = inter/256 blocks each; see row_geom); o[pos, r] = down[r] . h[pos].
+template <int TYPE, int TT, int WIDTH>
+__global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
+    ExpertView v;
+    if (!expert_view(a, blockIdx.y, false, v)) return;
+    constexpr int R = WIDTH == 64 ? 1 : 64 / WIDTH;
+    const int inter = static_cast<int>(v.stride_rows);
+    const int nb = inter / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
+    const int row_off = R > 1 ? g / nb : 0;
+    const int kb0 = R > 1 ? g % nb : g;
+    const int kb_step = R > 1 ? nb : 8;
+    const bool slot_used = R > 1 ? (g < R * nb) : true;
+    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R + row_off;
+    if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * R >= a.H) return;  // whole wave
+    const bool row_ok = slot_used && row < a.H;
+    const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
+    const uint8_t* wr = v.w + static_cast<int64_t>(row_ok ? row : 0) * rs;
+    const float* hin = v.routed ? a.h : a.h_sh;
+    float* oout = v.routed ? a.o : a.o_sh;
+    for (int p0 = v.begin; p0 < v.end; p0 += TT) {
+        float acc[TT];
+#pragma unroll
+        for (int u = 0; u < TT; u++) acc[u] = 0.0f;
+        if (row_ok) {
+            for (int kb = kb0; kb < nb; kb += kb_step) {
+                Lane32 l;
+                decode<TYPE>(wr + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, l);
+#pragma unroll
+                for (int u = 0; u < TT; u++) {
+                    if (p0 + u < v.end) {
+                        const float* hp = hin + static_cast<int64_t>(p0 + u) * inter + kb * kQK + lo_start;
+                        float4 xl[4], xh[4];
+                        load_run(hp, xl);
+                        load_run(hp + hi_off, xh);
+                        acc[u] += lane_dot(l, xl, xh);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+            const float s = group_sum<WIDTH>(acc[u]);
+            if ((lane & (WIDTH - 1)) == 0 && row_ok && p0 + u < v.end)
+                oout[static_cast<int64_t>(p0 + u) * a.H + row] = s;
+        }
+    }
+}
+
+// y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r].
+__global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int32_t* __restrict__ corder,
+                                                 const int32_t* __restrict__ pair_pos,
+                                                 const float* __restrict__ wts, const float* __restrict__ o,
+                                                 const float* __restrict__ o_sh, const float* __restrict__ sg,
+                                                 float* __restrict__ y) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int h4 = H / 4;
+    if (i >= static_cast<int64_t>(T) * h4) return;
+    const int t = static_cast<int>(i / h4);
+    const int r = static_cast<int>(i - static_cast<int64_t>(t) * h4) * 4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int n = 0; n < k; n++) {
+        const int s = corder[static_cast<int64_t>(t) * k + n];
+        const int64_t q = static_cast<int64_t>(t) * k + s;
+        const int pos = pair_pos[q];
+        if (pos < 0 || pos >= T * k) continue;  // never true for ids from k_topk; guards caller-supplied ids
+        const float wv = wts[q];
+        const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos) * H + r);
+        if (n == 0) {
+            acc = make_float4(wv * ov.x, wv * ov.y, wv * ov.z, wv * ov.w);
+        } else {
+            acc.x += wv * ov.x;
+            acc.y += wv * ov.y;
+            acc.z += wv * ov.z;
+            acc.w += wv * ov.w;
+        }
+    }
+    if (o_sh) {
+        const float gv = sg ? sg[t] : 1.0f;
+        const float4 sv = *reinterpret_cast<const float4*>(o_sh + static_cast<int64_t>(t) * H + r);
+        acc.x += gv * sv.x;
+        acc.y += gv * sv.y;
+        acc.z += gv * sv.z;
+        acc.w += gv * sv.w;
+    }
+    *reinterpret_cast<float4*>(y + static_cast<int64_t>(t) * H + r) = acc;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Host side
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves the workspace; with base == nullptr only computes the size.
+Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
+    Workspace w{};
+    const int64_t P = T * L.top_k;
+    const int64_t nchunks = (T + kSortChunk - 1) / kSortChunk;
+    const bool shared = L.shared_gate_up != nullptr;
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> void* {
+        void* p = base ? static_cast<char*>(base) + off : nullptr;
+        off = align_up(off + bytes, 256);
+        return p;
+    };
+    w.logits = static_cast<float*>(take(sizeof(float) * T * L.n_experts));
+    w.sg = static_cast<float*>(take(sizeof(float) * T));
+    w.ids = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.wts = static_cast<float*>(take(sizeof(float) * P));
+    w.corder = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.rank = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.hist = static_cast<int32_t*>(take(sizeof(int32_t) * nchunks * L.n_experts));
+    w.offsets = static_cast<int32_t*>(take(sizeof(int32_t) * (L.n_experts + 1)));
+    w.active = static_cast<int32_t*>(take(sizeof(int32_t) * (L.n_experts + 1)));
+    w.sorted = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.pair_pos = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.h = static_cast<float*>(take(sizeof(float) * P * L.inter));
+    w.o = static_cast<float*>(take(sizeof(float) * P * L.hidden));
+    w.h_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.shared_inter : 0));
+    w.o_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.hidden : 0));
+    w.bytes = off;
+    return w;
+}
+
+int check_layer(const WlMoeLayer* L) {
+    if (!L) return WL_EINVAL_NULL;
+    if (!L->gate_up || !L->down || !L->router) return WL_EINVAL_NULL;
+    if (block_bytes(L->gate_up_type) < 0 || block_bytes(L->down_type) < 0) return WL_EINVAL_TYPE;
+    if (L->hidden <= 0 || L->hidden % kQK != 0 || L->hidden > kRouterSeg * 32 * kRouterMaxJ) return WL_EINVAL_SHAPE;
+    if (L->inter <= 0 || L->inter % kQK != 0 || L->inter > kMaxK) return WL_EINVAL_SHAPE;
+    if (L->n_experts < 1 || L->n_experts > 64 * kMaxEJ) return WL_EINVAL_SHAPE;
+    if (L->top_k < 1 || L->top_k > L->n_experts || L->top_k > WL_MAX_TOPK) return WL_EINVAL_TOPK;
+    if (L->gate_up_stride < 2LL * L->inter * (L->hidden / kQK) * block_bytes(L->gate_up_type)) return WL_EINVAL_SHAPE;
+    if (L->down_stride < static_cast<int64_t>(L->hidden) * (L->inter / kQK) * block_bytes(L->down_type))
+        return WL_EINVAL_SHAPE;
+    if (reinterpret_cast<uintptr_t>(L->gate_up) % base_alignment(L->gate_up_type) ||
+        L->gate_up_stride % base_alignment(L->gate_up_type))
+        return WL_EINVAL_ALIGN;
+    if (reinterpret_cast<uintptr_t>(L->down) % base_alignment(L->down_type) ||
+        L->down_stride % base_alignment(L->down_type))
+        return WL_EINVAL_ALIGN;
+    if (reinterpret_cast<uintptr_t>(L->router) % 16) return WL_EINVAL_ALIGN;
+    if (L->shared_gate_up) {
+        if (!L->shared_down) return WL_EINVAL_NULL;
+        if (block_bytes(L->shared_gate_up_type) < 0 || block_bytes(L->shared_down_type) < 0) return WL_EINVAL_TYPE;
+        if (L->shared_inter <= 0 || L->shared_inter % kQK != 0 || L->shared_inter > kMaxK) return WL_EINVAL_SHAPE;
+        if (reinterpret_cast<uintptr_t>(L->shared_gate_up) % base_alignment(L->shared_gate_up_type) ||
+            reinterpret_cast<uintptr_t>(L->shared_down) % base_alignment(L->shared_down_type))
+            return WL_EINVAL_ALIGN;
+        if (L->shared_gate && reinterpret_cast<uintptr_t>(L->shared_gate) % 16) return WL_EINVAL_ALIGN;
+    }
+    return WL_OK;
+}
+
+static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s) {
+    const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
+    const int rows = L.n_experts + (shared_gate ? 1 : 0);
+    const int grid = (rows + 1) / 2;
+    if (T == 1)
+        k_router<1><<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, 1, L.hidden, L.n_experts, logits,
+                                         sg);
+    else
+        k_router<8><<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden,
+                                         L.n_experts, logits, sg);
+    return launch_status();
+}
+
+static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int32_t* ids, float* wts,
+                       int32_t* corder, hipStream_t s) {
+    const int grid = static_cast<int>((T + 3) / 4);
+    k_topk<<<grid, 256, 0, s>>>(logits, static_cast<int>(T), L.n_experts, L.top_k, L.norm_topk_prob ? 1 : 0, ids,
+                                 wts, corder);
+    return launch_status();
+}
+
+static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* ids, int64_t T, hipStream_t s) {
+    const int E = L.n_experts, k = L.top_k;
+    const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
+    const size_t scan_lds = sizeof(int32_t) * (3 * E + 2 * 256 + 1);
+    if (nchunks == 1) {
+        const size_t lds = sizeof(uint32_t) * E * kSortWords + scan_lds;
+        k_sort_small<<<1, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted, w.pair_pos);
+    } else {
+        const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
+        k_sort_hist<<<nchunks, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
+        k_sort_scan<<<1, 256, scan_lds + sizeof(int32_t) * E, s>>>(static_cast<int>(T), k, E, nchunks, w.hist,
+                                                                   w.offsets, w.active);
+        const int64_t P = T * k;
+        k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(ids, static_cast<int>(T), k, E, w.rank,
+                                                                          w.hist, w.sorted, w.pair_pos);
+    }
+    return launch_status();
+}
+
+template <int TYPE>
+static void launch_gate_up_t(const ExpertArgs& a, int rows, int slots, hipStream_t s) {
+    const dim3 grid((rows + 3) / 4, slots);
+    if (a.T == 1)
+        k_gate_up<TYPE, 1><<<grid, 256, 0, s>>>(a);
+    else
+        k_gate_up<TYPE, 4><<<grid, 256, 0, s>>>(a);
+}
+
+static void launch_gate_up(int type, const ExpertArgs& a, int rows, int slots, hipStream_t s) {
+    if (type == WL_TYPE_Q4_K)
+        launch_gate_up_t<WL_TYPE_Q4_K>(a, rows, slots, s);
+    else
+        launch_gate_up_t<WL_TYPE_Q6_K>(a, rows, slots, s);
+}
+
+template <int TYPE, int WIDTH>
+static void launch_down_w(const ExpertArgs& a, int slots, hipStream_t s) {
+    constexpr int R = WIDTH == 64 ? 1 : 64 / WIDTH;
+    const dim3 grid((a.H + 4 * R - 1) / (4 * R), slots);
+    if (a.T == 1)
+        k_down<TYPE, 1, WIDTH><<<grid, 256, 0, s>>>(a);
+    else
+        k_down<TYPE, 4, WIDTH><<<grid, 256, 0, s>>>(a);
+}
+
+template <int TYPE>
+static void launch_down_t(const ExpertArgs& a, int inter, int slots, hipStream_t s) {
+    switch (row_geom_width(inter / kQK)) {
+        case 8: launch_down_w<TYPE, 8>(a, slots, s); break;
+        case 16: launch_down_w<TYPE, 16>(a, slots, s); break;
+        case 32: launch_down_w<TYPE, 32>(a, slots, s); break;
+        default: launch_down_w<TYPE, 64>(a, slots, s); break;
+    }
+}
+
+static void launch_down(int type, const ExpertArgs& a, int inter, int slots, hipStream_t s) {
+    if (type == WL_TYPE_Q4_K)
+        launch_down_t<WL_TYPE_Q4_K>(a, inter, slots, s);
+    else
+        launch_down_t<WL_TYPE_Q6_K>(a, inter, slots, s);
+}
+
+}  // namespace wl
+
+using namespace wl;
+
+extern "C" {
+
+const char* wl_error_string(int code) {
+    switch (code) {
+        case WL_OK: return "ok";
+        case WL_EINVAL_TYPE: return "unsupported ggml type (only Q4_K = 12 and Q6_K = 14 run here)";
+        case WL_EINVAL_SHAPE: return "invalid shape: sizes must be positive, k a multiple of 256, within limits";
+        case WL_EINVAL_NULL: return "a required pointer is NULL";
+        case WL_EINVAL_ALIGN: return "misaligned pointer or stride (Q4_K: 16 bytes; Q6_K: 4; activations: 16)";
+        case WL_EINVAL_TOPK: return "top_k must be in 1..min(n_experts, 16)";
+        case WL_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wl_moe_workspace_bytes()";
+        case WL_EINVAL_DTYPE: return "output dtype must be WL_DTYPE_F32 or WL_DTYPE_BF16";
+        case WL_EINVAL_COUNT: return "expert count must be in 1..64";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown error";
+}
+
+int wl_abi_version(void) { return (1 << 16) | 0; }
+
+int wl_moe_check(const WlMoeLayer* layer) { return check_layer(layer); }
+
+size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens) {
+    if (check_layer(layer) != WL_OK || tokens <= 0) return 0;
+    return carve(*layer, tokens, nullptr).bytes;
+}
+
+int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float* logits, int32_t* ids,
+                 float* weights, float* shared_gate_out, void* stream) {
+    int rc = check_layer(layer);
+    if (rc) return rc;
+    if (!x || !logits || !ids || !weights) return WL_EINVAL_NULL;
+    if (layer->shared_gate_up && layer->shared_gate && !shared_gate_out) return WL_EINVAL_NULL;
+    if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16) return WL_EINVAL_ALIGN;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = launch_router(*layer, x, tokens, logits, shared_gate_out, s);
+    if (rc) return rc;
+    return launch_topk(*layer, logits, tokens, ids, weights, nullptr, s);
+}
+
+static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
+                     float* weights, void* workspace, size_t workspace_bytes, void* stream, void* const* events) {
+    int rc = check_layer(layer);
+    if (rc) return rc;
+    if (!x || !y) return WL_EINVAL_NULL;
+    if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16) return WL_EINVAL_ALIGN;
+    const WlMoeLayer& L = *layer;
+    const Workspace need = carve(L, tokens, nullptr);
+    if (!workspace || workspace_bytes < need.bytes) return WL_EINVAL_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return WL_EINVAL_ALIGN;
+    Workspace w = carve(L, tokens, workspace);
+    if (ids) w.ids = ids;
+    if (weights) w.wts = weights;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool shared = L.shared_gate_up != nullptr;
+    float* sg = (shared && L.shared_gate) ? w.sg : nullptr;
+
+    // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
+    auto mark = [&](int i) {
+        if (events) (void)hipEventRecord(static_cast<hipEvent_t>(events[i]), s);
+    };
+    mark(0);
+    rc = launch_router(L, x, tokens, w.logits, sg, s);
+    if (rc) return rc;
+    mark(1);
+    rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
+    if (rc) return rc;
+    mark(2);
+    rc = launch_sort(L, w, w.ids, tokens, s);
+    if (rc) return rc;
+    mark(3);
+
+    ExpertArgs a{};
+    a.gate_up = static_cast<const uint8_t*>(L.gate_up);
+    a.gate_up_stride = L.gate_up_stride;
+    a.down = static_cast<const uint8_t*>(L.down);
+    a.down_stride = L.down_stride;
+    a.sh_gate_up = static_cast<const uint8_t*>(L.shared_gate_up);
+    a.sh_down = static_cast<const uint8_t*>(L.shared_down);
+    a.x = x;
+    a.T = static_cast<int>(tokens);
+    a.H = L.hidden;
+    a.inter = L.inter;
+    a.sh_inter = shared ? L.shared_inter : 0;
+    a.k = L.top_k;
+    a.offsets = w.offsets;
+    a.active = w.active;
+    a.sorted = w.sorted;
+    a.h = w.h;
+    a.h_sh = w.h_sh;
+    a.o = w.o;
+    a.o_sh = w.o_sh;
+    const int max_active = static_cast<int>(tokens * L.top_k < L.n_experts ? tokens * L.top_k : L.n_experts);
+
+    // gate_up + SwiGLU: routed experts, then (same kernel when the types agree) the shared expert
+    const bool fuse_gu = shared && L.shared_gate_up_type == L.gate_up_type && L.shared_inter == L.inter;
+    a.n_routed = max_active;
+    launch_gate_up(L.gate_up_type, a, L.inter, max_active + (fuse_gu ? 1 : 0), s);
+    if (shared && !fuse_gu) {
+        ExpertArgs b = a;
+        b.n_routed = 0;
+        launch_gate_up(L.shared_gate_up_type, b, L.shared_inter, 1, s);
+    }
+    const bool fuse_dn = shared && L.shared_down_type == L.down_type && L.shared_inter == L.inter;
+    mark(4);
+    launch_down(L.down_type, a, L.inter, max_active + (fuse_dn ? 1 : 0), s);
+    if (shared && !fuse_dn) {
+        ExpertArgs b = a;
+        b.n_routed = 0;
+        launch_down(L.shared_down_type, b, L.shared_inter, 1, s);
+    }
+    rc = launch_status();
+    if (rc) return rc;
+    mark(5);
+    const int64_t threads = tokens * (L.hidden / 4);
+    k_combine<<<static_cast<int>((threads + 255) / 256), 256, 0, s>>>(
+        static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos, w.wts, w.o, shared ? w.o_sh : nullptr,
+        sg, y);
+    rc = launch_status();
+    mark(6);
+    return rc;
+}
+
+int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+    return run_layer(layer, x, tokens, y, ids, weights, workspace, workspace_bytes, stream, nullptr);
+}
+
+int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
+                         float* weights, void* workspace, size_t workspace_bytes, void* stream,
+                         void* const* events_host) {
+    if (!events_host) return WL_EINVAL_NULL;
+    for (int i = 0; i <= kMoeStages; i++)
+        if (!events_host[i]) return WL_EINVAL_NULL;
+    return run_layer(layer, x, tokens, y, ids, weights, workspace, workspace_bytes, stream, events_host);
+}
+
+int wl_moe_stage_count(void) { return kMoeStages; }
+
+const char* wl_moe_stage_name(int stage) {
+    static const char* names[kMoeStages] = {"router", "topk", "sort", "gate_up", "down", "combine"};
+    return stage >= 0 && stage < kMoeStages ? names[stage] : "";
+}
+
+}  // extern "C"

@@ -1,0 +1,121 @@
+"""The fused MoE layer (wl_moe_layer): one call runs the router, top-k, token->expert grouping, the SwiGLU experts
+and the weighted combine with the shared expert, all on the GPU with no host synchronization. This is
+Engine.moe (engines/base.py:445-490) without its `.cpu()` dispatch (:456-460).
+"""
+import ctypes
+
+import torch
+
+from . import (TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class MoELayer:
+    """One MoE layer's weights in device memory and the call that runs it.
+
+    gate_up: uint8 [n_experts, 2*inter * row_bytes(gate_up_type, hidden)], each expert's fused [gate | up] matrix
+             (gate rows first, gguf/compiler.py:69-88); down: uint8 [n_experts, hidden * row_bytes(down_type,
+             inter)]; router: fp32 [n_experts, hidden]; router_bias: fp32 [n_experts] or None; shared_gate_up,
+             shared_down: the shared expert's matrices (or None); shared_gate: fp32 [hidden] or None.
+    Tensors may be views into a larger store; each expert's bytes must be contiguous (a row of a 2-D tensor)."""
+
+    def __init__(self, *, gate_up, down, router, hidden: int, inter: int, n_experts: int, top_k: int,
+                 norm_topk_prob: bool = True, gate_up_type: str = "Q4_K", down_type: str = "Q6_K",
+                 router_bias=None, shared_gate_up=None, shared_down=None, shared_gate=None, shared_inter=None,
+                 shared_gate_up_type=None, shared_down_type=None):
+        for name, t in (("gate_up", gate_up), ("down", down), ("router", router)):
+            _on_gpu(t, name)
+        if router.dtype != torch.float32:
+            raise ValueError("router weights must be fp32 [n_experts, hidden]")
+        self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
+        self.norm_topk_prob = bool(norm_topk_prob)
+        self.gate_up_type, self.down_type = gate_up_type, down_type
+        self.shared_inter = shared_inter if shared_inter is not None else inter
+        self.shared_gate_up_type = shared_gate_up_type or gate_up_type
+        self.shared_down_type = shared_down_type or down_type
+        gu_bytes = 2 * inter * row_bytes(gate_up_type, hidden)
+        dn_bytes = hidden * row_bytes(down_type, inter)
+        self.gate_up = gate_up.reshape(n_experts, -1)
+        self.down = down.reshape(n_experts, -1)
+        if self.gate_up.shape[1] < gu_bytes or self.down.shape[1] < dn_bytes:
+            raise ValueError("expert tensors are smaller than their shapes need")
+        self.router = router.contiguous()
+        self.router_bias = None if router_bias is None else router_bias.to(torch.float32).contiguous()
+        self.shared_gate_up = shared_gate_up
+        self.shared_down = shared_down
+        self.shared_gate = None if shared_gate is None else shared_gate.to(torch.float32).reshape(-1).contiguous()
+        self.device = router.device
+        self._ws = None
+        s = WlMoeLayer()
+        s.gate_up, s.down, s.router = self.gate_up.data_ptr(), self.down.data_ptr(), self.router.data_ptr()
+        s.router_bias = _ptr(self.router_bias)
+        s.shared_gate_up, s.shared_down = _ptr(shared_gate_up), _ptr(shared_down)
+        s.shared_gate = _ptr(self.shared_gate)
+        s.gate_up_stride = self.gate_up.stride(0) * self.gate_up.element_size()
+        s.down_stride = self.down.stride(0) * self.down.element_size()
+        s.gate_up_type, s.down_type = _type_id(gate_up_type), _type_id(down_type)
+        s.shared_gate_up_type = TYPE_IDS.get(self.shared_gate_up_type, -1)
+        s.shared_down_type = TYPE_IDS.get(self.shared_down_type, -1)
+        s.hidden, s.inter, s.shared_inter = hidden, inter, self.shared_inter
+        s.n_experts, s.top_k, s.norm_topk_prob = n_experts, top_k, int(self.norm_topk_prob)
+        self.struct = s
+        check(library().wl_moe_check(ctypes.byref(s)))
+
+    @classmethod
+    def from_host(cls, lw: dict, device="cuda"):
+        """From a layer dict of numpy arrays (gguf.synth.moe_layer's layout), copied to the GPU."""
+        def dev(a):
+            return None if a is None else torch.from_numpy(a).to(device)
+        return cls(gate_up=dev(lw["gate_up"].reshape(lw["experts"], -1)),
+                   down=dev(lw["down"].reshape(lw["experts"], -1)), router=dev(lw["router"]),
+                   router_bias=dev(lw.get("router_bias")), hidden=lw["hidden"], inter=lw["inter"],
+                   n_experts=lw["experts"], top_k=lw["top_k"], norm_topk_prob=lw["norm_topk_prob"],
+                   gate_up_type=lw["gate_up_type"], down_type=lw["down_type"],
+                   shared_gate_up=dev(lw.get("shared_gate_up")), shared_down=dev(lw.get("shared_down")),
+                   shared_gate=dev(lw.get("shared_gate")), shared_inter=lw.get("shared_inter"),
+                   shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"))
+
+    def workspace_bytes(self, tokens: int) -> int:
+        return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
+
+    def workspace(self, tokens: int) -> torch.Tensor:
+        need = self.workspace_bytes(tokens)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor = None, ids: torch.Tensor = None,
+                 weights: torch.Tensor = None, workspace: torch.Tensor = None) -> torch.Tensor:
+        """x [T, hidden] -> fp32 [T, hidden] (written into `out` when given). ids int32 / weights fp32 [T, top_k]
+        receive the routing when given."""
+        _on_gpu(x, "x")
+        xf = x.reshape(-1, self.hidden).to(torch.float32).contiguous()
+        tokens = xf.shape[0]
+        y = out if out is not None else torch.empty(tokens, self.hidden, dtype=torch.float32, device=self.device)
+        ws = workspace if workspace is not None else self.workspace(tokens)
+        check(library().wl_moe_layer(ctypes.byref(self.struct), xf.data_ptr(), tokens, y.data_ptr(), _ptr(ids),
+                                     _ptr(weights), ws.data_ptr(), ws.numel(), _stream(self.device)))
+        return y
+
+    def route(self, x: torch.Tensor):
+        """-> (weights fp32 [T, top_k], ids int32 [T, top_k], shared gate fp32 [T] or None): engines/base.py:91-97
+        on the router logits, plus sigmoid(x . shared_gate)."""
+        xf = x.reshape(-1, self.hidden).to(torch.float32).contiguous()
+        tokens = xf.shape[0]
+        logits = torch.empty(tokens, self.n_experts, dtype=torch.float32, device=self.device)
+        ids = torch.empty(tokens, self.top_k, dtype=torch.int32, device=self.device)
+        weights = torch.empty(tokens, self.top_k, dtype=torch.float32, device=self.device)
+        sg = None
+        if self.shared_gate_up is not None and self.shared_gate is not None:
+            sg = torch.empty(tokens, dtype=torch.float32, device=self.device)
+        check(library().wl_moe_route(ctypes.byref(self.struct), xf.data_ptr(), tokens, logits.data_ptr(),
+                                     ids.data_ptr(), weights.data_ptr(), _ptr(sg), _stream(self.device)))
+        return weights, ids, sg
+
+
+def moe_layer(x: torch.Tensor, layer: MoELayer) -> torch.Tensor:
+    """The whole layer in one call: y = MoE(x) as fp32."""
+    return layer(x)
