@@ -94,13 +94,28 @@ typedef struct WlMoeLayer {
     int32_t gate_up_type, down_type, shared_gate_up_type, shared_down_type;
     int32_t hidden, inter, shared_inter;
     int32_t n_experts, top_k, norm_topk_prob;
+    int32_t flags;               /* WL_MOE_* bits; 0 = defaults */
+    int32_t reserved;            /* 0 */
 } WlMoeLayer;
+
+#define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */
 
 /* Checks a layer description without touching device memory; 0 or a WL_E* code. */
 int wl_moe_check(const WlMoeLayer* layer);
 
 /* Bytes of device workspace wl_moe_layer needs for `tokens` tokens (0 on an invalid layer). */
 size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
+
+/* Zeroes the synchronization words at the start of a workspace (the fused decode kernel's grid-barrier flags,
+ * about 64 KiB) with a fill kernel on `stream`. Call once after allocating a workspace, before its first
+ * wl_moe_layer; calls keep these words consistent afterwards. Calls that share one workspace must be ordered (one
+ * stream): concurrent ones race. */
+int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Which path wl_moe_layer takes for `tokens` tokens: 1 = one fused persistent kernel (batch-1 decode at
+ * Qwen3.6-like shapes), 0 = the multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an
+ * invalid layer. */
+int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens);
 
 /* Router: logits = x W_r^T (+ bias) in a fixed floating-point order: hidden is cut into segments of 64
  * consecutive values; each segment's partial is a chain of fused multiply-adds in ascending index starting from 0;
@@ -121,7 +136,8 @@ int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* wl_moe_layer with a hipEvent_t recorded on `stream` at every stage boundary: events_host[i] just before stage i,
- * events_host[wl_moe_stage_count()] after the last (so wl_moe_stage_count() + 1 events, none NULL). For per-stage
+ * events_host[wl_moe_stage_count()] after the last (so wl_moe_stage_count() + 1 events, none NULL). On the fused
+ * path (wl_moe_plan() == 1) stage 0 holds the single fused kernel and the other stages are empty. For per-stage
  * timing with hipEventElapsedTime; do not use under stream capture. No counterpart in the reference, whose only
  * timers are host-side (engines/base.py:384-390). */
 int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,

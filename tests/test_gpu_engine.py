@@ -1,0 +1,87 @@
+"""The drop-in: Engine.moe through the HipMoE mixin on an HBM-resident expert store, against the CPU oracle, with
+the engine attributes and weight names the reference's Engine uses (engines/base.py:285-286,445-490)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gguf import synth
+from gguf.hbm_store import HBMExpertStore
+from gguf.hip import GGMLWeight
+from engines.qwen36 import HipMoE
+from oracle import moe_ref
+from oracle import quants_ref as q
+
+pytestmark = pytest.mark.gpu
+PREFIX = "model.language_model."
+
+
+class TinyEngine(HipMoE):
+    """The attributes Engine.moe reads, nothing else."""
+    prefix = PREFIX
+
+    def __init__(self, store, weights, top_k, norm=True):
+        self.experts, self.weights, self.top_k, self.norm_topk_prob = store, weights, top_k, norm
+
+
+def engine_weights(lw, layer=0, quantized_shared=True):
+    p = f"{PREFIX}layers.{layer}.mlp"
+    H, I = lw["hidden"], lw["shared_inter"]
+    w = {p + ".gate.weight": torch.from_numpy(lw["router"]).cuda(),
+         p + ".shared_expert_gate.weight": torch.from_numpy(lw["shared_gate"][None]).cuda()}
+    gu = lw["shared_gate_up"]
+    if quantized_shared:
+        rb = q.row_bytes("Q4_K", H)
+        w[p + ".shared_expert.gate_proj.weight"] = GGMLWeight(torch.from_numpy(gu[:I].reshape(-1)).cuda(), "Q4_K", (I, H))
+        w[p + ".shared_expert.up_proj.weight"] = GGMLWeight(torch.from_numpy(gu[I:].reshape(-1)).cuda(), "Q4_K", (I, H))
+        w[p + ".shared_expert.down_proj.weight"] = GGMLWeight(
+            torch.from_numpy(lw["shared_down"].reshape(-1)).cuda(), lw["shared_down_type"], (H, I))
+        assert gu.shape[1] == rb
+    else:
+        dq = q.dequantize_matrix(gu, "Q4_K", 2 * I, H)
+        w[p + ".shared_expert.gate_proj.weight"] = torch.from_numpy(dq[:I]).cuda()
+        w[p + ".shared_expert.up_proj.weight"] = torch.from_numpy(dq[I:]).cuda()
+        w[p + ".shared_expert.down_proj.weight"] = torch.from_numpy(
+            q.dequantize_matrix(lw["shared_down"], lw["shared_down_type"], H, I)).cuda()
+    return w
+
+
+@pytest.fixture(scope="module")
+def small_layer():
+    return synth.moe_layer(61, hidden=2048, inter=512, shared_inter=512, experts=64, top_k=8)
+
+
+@pytest.mark.parametrize("quantized_shared", [True, False])
+@pytest.mark.parametrize("tokens", [1, 9])
+def test_engine_moe_matches_oracle(small_layer, quantized_shared, tokens):
+    lw = small_layer
+    store = HBMExpertStore.from_host([lw])
+    eng = TinyEngine(store, engine_weights(lw, quantized_shared=quantized_shared), lw["top_k"])
+    x = synth.tokens(62 + tokens, tokens)
+    y = eng.moe(torch.from_numpy(x).cuda(), 0, residual=None)
+    assert y.shape == (tokens, 2048) and y.dtype == torch.float32
+    assert moe_ref.rel_err(y.cpu().numpy(), moe_ref.layer(x, lw)) < 2e-3
+    yb = eng.moe(torch.from_numpy(x).cuda().to(torch.bfloat16), 0)
+    assert yb.dtype == torch.bfloat16
+
+
+def test_store_surface(small_layer):
+    """load_many / load_batches hand out GGMLWeight views that F.linear runs (engines/base.py:552-571)."""
+    lw = small_layer
+    store = HBMExpertStore.from_host([lw])
+    assert store.runs_batched(0)
+    assert store.nbytes() == lw["gate_up"].nbytes + lw["down"].nbytes
+    x = torch.from_numpy(synth.tokens(5, 1)).cuda()
+    (batch,) = list(store.load_batches(0, [3, 17]))
+    assert [e for e, _ in batch] == [3, 17]
+    for e, (gate_up, down) in store.load_many(0, [3, 17]):
+        gu = F.linear(x, gate_up)
+        h = F.silu(gu[:, :512]) * gu[:, 512:]
+        y = F.linear(h, down).cpu().numpy()
+        ref = moe_ref.expert_ffn(x.cpu().numpy(), q.dequantize_matrix(lw["gate_up"][e], "Q4_K", 1024, 2048),
+                                 q.dequantize_matrix(lw["down"][e], "Q6_K", 2048, 512), 512)
+        assert moe_ref.rel_err(y, ref) < 2e-3
+        base, off = gate_up.location()
+        assert off == e * lw["gate_up"][0].nbytes
+    store.record_usage(0, torch.tensor([[3, 17], [3, 5]]))
+    assert int(store.usage[0][3]) == 2

@@ -53,6 +53,35 @@ def test_layer_c2_decode_b1(hip, c2, layer_c2):
     check_layer(hip, c2, layer_c2, synth.tokens(2, 1), "c2 b=1")
 
 
+def test_fused_matches_multi_kernel(hip, c2, layer_c2):
+    """Batch-1 decode runs as one fused persistent kernel; it must give the multi-kernel path's routing bits and
+    its outputs up to the compiler's multiply-add contraction in the combine (~1e-6)."""
+    multi = hip.MoELayer.from_host(layer_c2, fused=False)
+    assert c2.plan(1) == "fused" and multi.plan(1) == "multi" and c2.plan(2) == "multi"
+    for seed in range(5):
+        x = synth.tokens(200 + seed, 1)
+        y_f, ids_f, w_f = run_layer(hip, c2, x)
+        y_m, ids_m, w_m = run_layer(hip, multi, x)
+        np.testing.assert_array_equal(ids_f, ids_m)
+        np.testing.assert_array_equal(w_f, w_m)
+        assert moe_ref.rel_err(y_f, y_m) < 1e-5
+
+
+def test_fused_back_to_back(hip, c2, layer_c2):
+    """Many fused calls in a row on one workspace (the grid barrier's words must reset each time), checked
+    against the oracle at the end."""
+    x = synth.tokens(300, 16)
+    xs = torch.from_numpy(x).cuda()
+    ys = torch.empty(16, 2048, device="cuda")
+    ws = c2.workspace(1)
+    for i in range(16):
+        c2(xs[i:i + 1], out=ys[i:i + 1], workspace=ws)
+    torch.cuda.synchronize()
+    y_ref = moe_ref.layer(x, layer_c2)
+    assert np.isfinite(ys.cpu().numpy()).all()
+    assert moe_ref.rel_err(ys.cpu().numpy(), y_ref) < TOL
+
+
 def test_layer_c2_repeatable(hip, c2, layer_c2):
     x = synth.tokens(3, 4)
     a = run_layer(hip, c2, x)[0]

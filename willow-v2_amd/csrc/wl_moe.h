@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <hip/hip_runtime.h>
+
 #include "../../include/willow_hip.h"
 
 namespace wl {
@@ -15,6 +17,12 @@ constexpr int kSortChunk = 256;    // grouping: tokens per bitmap chunk
 constexpr int kSortWords = kSortChunk / 32;
 constexpr int64_t kMaxTokens = 1 << 20;
 constexpr int kMoeStages = 6;  // router, topk, sort, gate_up, down, combine
+constexpr int kFusedMaxK = 8;     // fused decode kernel: most experts per token
+constexpr int kFusedMaxG = 512;   // fused decode kernel: most workgroups (one per CU)
+constexpr int kFlagStride = 32;   // fused decode kernel: words between workgroup flags (one 128-byte line each)
+// fused decode kernel: synchronization words at the start of the workspace (release word, one flag line per
+// workgroup, the routing)
+constexpr int kSyncWords = kFlagStride * (1 + kFusedMaxG) + 2 * kFusedMaxK + 1;
 
 struct ExpertArgs {
     const uint8_t* gate_up;
@@ -36,7 +44,8 @@ struct ExpertArgs {
 };
 
 struct Workspace {
-    float* logits;      // [T, E]
+    uint32_t* sync;     // [kSyncWords] grid-barrier words of the fused kernel (zeroed once, left zeroed)
+    float* logits;      // [T, E + 1]
     float* sg;          // [T]      sigmoid(shared gate)
     int32_t* ids;       // [T, k]
     float* wts;         // [T, k]
@@ -56,5 +65,9 @@ struct Workspace {
 
 Workspace carve(const WlMoeLayer& L, int64_t T, void* base);
 int check_layer(const WlMoeLayer* L);
+bool fused_eligible(const WlMoeLayer& L, int64_t T);
+int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,
+                 hipStream_t s);
+int zero_sync(void* workspace, hipStream_t s);
 
 }  // namespace wl

@@ -6,6 +6,7 @@
 #include "wl_common.h"
 #include "wl_host.h"
 #include "wl_moe.h"
+#include "wl_moe_dev.h"
 
 namespace wl {
 
@@ -81,75 +82,43 @@ __global__ __launch_bounds__(64) void k_router(const float* __restrict__ x, cons
     }
 }
 
+// One token: the shared router_row (the fused decode kernel computes the same rows with it).
+__global__ __launch_bounds__(64) void k_router1(const float* __restrict__ x, const float* __restrict__ w,
+                                                const float* __restrict__ bias,
+                                                const float* __restrict__ shared_gate, int H, int E,
+                                                float* __restrict__ logits, float* __restrict__ sg) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 2 + (lane >> 5);
+    const int rows_total = E + (shared_gate ? 1 : 0);
+    const bool valid = row < rows_total;
+    const float* wr = row < E ? w + static_cast<int64_t>(row) * H : shared_gate;
+    const float total = router_row(x, wr, valid, H, lane);
+    if ((lane & 31) == 0 && valid) {
+        if (row < E)
+            logits[row] = bias ? __fadd_rn(total, bias[row]) : total;
+        else
+            sg[0] = sigmoid(total);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
-// Top-k: one wavefront per token. Softmax over all E in fp32; selection on the logits (softmax is monotone),
-// largest first, ties to the lower expert id; weights p_r = exp(l_r - max) / sum, renormalized over the k picks
-// when requested (engines/base.py:91-97). corder[t, i] = the slot of the token's i-th smallest expert id, the
+// Top-k: one wavefront per token (wave_topk). corder[t, i] = the slot of the token's i-th smallest expert id, the
 // order the combine adds experts in.
+template <int EJ>
 __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, int T, int E, int k, int renorm,
                                               int32_t* __restrict__ ids, float* __restrict__ wts,
                                               int32_t* __restrict__ corder) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ uint32_t scratch[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wv;
     if (t >= T) return;
-    const float* lt = logits + static_cast<int64_t>(t) * E;
-    float v[kMaxEJ];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMaxEJ; j++) {
-        const int idx = lane + 64 * j;
-        const float lv = idx < E ? lt[idx] : -INFINITY;
-        v[j] = lv == lv ? lv : -INFINITY;  // a NaN logit ranks last, so k valid ids are always picked
-        m = fmaxf(m, v[j]);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxEJ; j++)
-        if (lane + 64 * j < E) s += expf(v[j] - m);
-    s = group_sum<64>(s);
-    uint32_t taken = 0;
-    int my_id = 0;
-    float my_v = -INFINITY;
-    for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < kMaxEJ; j++) {
-            const int idx = lane + 64 * j;
-            if (idx < E && !((taken >> j) & 1u) && (v[j] > bv || (v[j] == bv && idx < bi))) {
-                bv = v[j];
-                bi = idx;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (lane == r) {
-            my_id = bi;
-            my_v = bv;
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    }
-    const float p = lane < k ? expf(my_v - m) / s : 0.0f;
-    float wsum = 0.0f;
-    for (int r = 0; r < k; r++) {
-        const float pr = __shfl(p, r);
-        wsum = r == 0 ? pr : wsum + pr;
-    }
-    int rank = 0;
-    for (int r = 0; r < k; r++) rank += __shfl(my_id, r) < my_id ? 1 : 0;
+    int id, id_rank;
+    float w;
+    wave_topk<EJ>(logits + static_cast<int64_t>(t) * E, E, k, renorm != 0, scratch[wv], lane, id, w, id_rank);
     if (lane < k) {
-        ids[static_cast<int64_t>(t) * k + lane] = my_id;
-        wts[static_cast<int64_t>(t) * k + lane] = renorm ? p / wsum : p;
-        if (corder) corder[static_cast<int64_t>(t) * k + rank] = lane;
+        ids[static_cast<int64_t>(t) * k + lane] = id;
+        wts[static_cast<int64_t>(t) * k + lane] = w;
+        if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
     }
 }
 
@@ -368,6 +337,17 @@ __global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a) {
     const int inter = static_cast<int>(v.stride_rows);
     const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (j >= inter) return;
+    if constexpr (TT == 1) {  // one token per expert: the shared gate_up_row, as the fused decode kernel
+        const int lane1 = threadIdx.x & 63;
+        for (int pos = v.begin; pos < v.end; pos++) {
+            const int tok = v.routed ? a.sorted[pos] / a.k : pos;
+            float gs, us;
+            gate_up_row<TYPE>(v.w, j, inter, a.H, a.x + static_cast<int64_t>(tok) * a.H, lane1, gs, us);
+            if (lane1 == 0) (v.routed ? a.h : a.h_sh)[static_cast<int64_t>(v.routed ? pos : tok) * inter + j] =
+                silu(gs) * us;
+        }
+        return;
+    }
     const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
@@ -520,7 +500,8 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
         off = align_up(off + bytes, 256);
         return p;
     };
-    w.logits = static_cast<float*>(take(sizeof(float) * T * L.n_experts));
+    w.sync = static_cast<uint32_t*>(take(sizeof(uint32_t) * kSyncWords));
+    w.logits = static_cast<float*>(take(sizeof(float) * T * (L.n_experts + 1)));
     w.sg = static_cast<float*>(take(sizeof(float) * T));
     w.ids = static_cast<int32_t*>(take(sizeof(int32_t) * P));
     w.wts = static_cast<float*>(take(sizeof(float) * P));
@@ -574,8 +555,7 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
     const int rows = L.n_experts + (shared_gate ? 1 : 0);
     const int grid = (rows + 1) / 2;
     if (T == 1)
-        k_router<1><<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, 1, L.hidden, L.n_experts, logits,
-                                         sg);
+        k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
     else
         k_router<8><<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden,
                                          L.n_experts, logits, sg);
@@ -585,8 +565,17 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
 static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int32_t* ids, float* wts,
                        int32_t* corder, hipStream_t s) {
     const int grid = static_cast<int>((T + 3) / 4);
-    k_topk<<<grid, 256, 0, s>>>(logits, static_cast<int>(T), L.n_experts, L.top_k, L.norm_topk_prob ? 1 : 0, ids,
-                                 wts, corder);
+    const int E = L.n_experts, k = L.top_k, rn = L.norm_topk_prob ? 1 : 0, Ti = static_cast<int>(T);
+    if (E <= 64)
+        k_topk<1><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+    else if (E <= 128)
+        k_topk<2><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+    else if (E <= 256)
+        k_topk<4><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+    else if (E <= 512)
+        k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+    else
+        k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
     return launch_status();
 }
 
@@ -715,11 +704,18 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool shared = L.shared_gate_up != nullptr;
     float* sg = (shared && L.shared_gate) ? w.sg : nullptr;
-
-    // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
-    auto mark = [&](int i) {
+    auto record = [&](int i) {
         if (events) (void)hipEventRecord(static_cast<hipEvent_t>(events[i]), s);
     };
+    if (fused_eligible(L, tokens)) {  // one launch: the whole layer (stage 0 of a profile holds it)
+        record(0);
+        rc = launch_fused(L, x, y, ids, weights, w, s);
+        for (int i = 1; i <= kMoeStages; i++) record(i);
+        return rc;
+    }
+
+    // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
+    auto mark = record;
     mark(0);
     rc = launch_router(L, x, tokens, w.logits, sg, s);
     if (rc) return rc;
@@ -797,6 +793,18 @@ int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens
 }
 
 int wl_moe_stage_count(void) { return kMoeStages; }
+
+int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens) {
+    if (check_layer(layer) != WL_OK || tokens <= 0) return -1;
+    return fused_eligible(*layer, tokens) ? 1 : 0;
+}
+
+int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+    if (!workspace) return WL_EINVAL_NULL;
+    if (workspace_bytes < sizeof(uint32_t) * kSyncWords) return WL_EINVAL_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return WL_EINVAL_ALIGN;
+    return zero_sync(workspace, static_cast<hipStream_t>(stream));
+}
 
 const char* wl_moe_stage_name(int stage) {
     static const char* names[kMoeStages] = {"router", "topk", "sort", "gate_up", "down", "combine"};

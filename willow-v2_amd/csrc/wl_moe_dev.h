@@ -1,0 +1,183 @@
+// Device functions shared by the multi-kernel MoE path (wl_moe.hip) and the fused decode kernel
+// (wl_moe_fused.hip), so both compute bit-identical logits, routing, SwiGLU rows and down rows.
+#pragma once
+
+#include "wl_common.h"
+#include "wl_moe.h"
+
+namespace wl {
+
+// One token's router logits for two rows at once: lanes [0, 32) work on row `row` of their half, lanes [32, 64)
+// on the other half's row; each lane owns the 64-value segments s = slot, slot + 32, ... and chains fused
+// multiply-adds over them in ascending k; the segment partials are then added left to right. Every lane of a
+// half returns its row's sum (no bias). Call with the whole wavefront; `valid` may differ between the halves.
+__device__ __forceinline__ float router_row(const float* __restrict__ x, const float* __restrict__ wr, bool valid,
+                                            int H, int lane) {
+    const int slot = lane & 31, src_base = lane & 32;
+    const int nseg = H / kRouterSeg;
+    float p[kRouterMaxJ];
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; j++) p[j] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; j++) {
+        const int s = slot + 32 * j;
+        if (valid && s < nseg) {
+            const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
+            const float4* xp = reinterpret_cast<const float4*>(x + s * kRouterSeg);
+#pragma unroll
+            for (int i = 0; i < kRouterSeg / 4; i++) {
+                const float4 wv = wp[i], xv = xp[i];
+                p[j] = __builtin_fmaf(xv.x, wv.x, p[j]);
+                p[j] = __builtin_fmaf(xv.y, wv.y, p[j]);
+                p[j] = __builtin_fmaf(xv.z, wv.z, p[j]);
+                p[j] = __builtin_fmaf(xv.w, wv.w, p[j]);
+            }
+        }
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; j++) {
+        if (32 * j < nseg) {
+            for (int sl = 0; sl < 32; sl++) {
+                const int s = sl + 32 * j;
+                if (s < nseg) {
+                    const float v = __shfl(p[j], src_base + sl);
+                    total = s == 0 ? v : __fadd_rn(total, v);
+                }
+            }
+        }
+    }
+    return total;
+}
+
+// float -> uint32 with the same order (larger float, larger key)
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Top-k of one token's logits (lt[0..E), E <= 64*EJ), one wavefront. Softmax over all E in fp32; the selection is
+// on the logits (softmax is monotone): largest first, ties to the lower expert id, NaN ranked as -inf. Lane r < k
+// returns the r-th pick: its expert id, its weight exp(l - max) / sum (divided by the sum of the k picks' weights,
+// added in pick order, when renorm), and id_rank = its position among the k ids in ascending order.
+// The k-th largest key is found by a bitwise radix select over ballots (32 steps, no cross-lane latency chain);
+// the k picks are then compacted and ranked through `scratch` (64 words of LDS owned by this wavefront).
+template <int EJ>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, int k, bool renorm,
+                                          volatile uint32_t* scratch, int lane, int& out_id, float& out_w,
+                                          int& out_id_rank) {
+    float v[EJ];
+    uint32_t key[EJ];
+    bool valid[EJ];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EJ; j++) {
+        const int idx = lane + 64 * j;
+        valid[j] = idx < E;
+        const float lv = valid[j] ? lt[idx] : -INFINITY;
+        v[j] = lv == lv ? lv : -INFINITY;
+        key[j] = order_key(v[j]);
+        m = fmaxf(m, v[j]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EJ; j++)
+        if (valid[j]) s += expf(v[j] - m);
+    s = group_sum<64>(s);
+
+    uint32_t K = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = K | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < EJ; j++) cnt += __popcll(__ballot(valid[j] && key[j] >= cand));
+        if (cnt >= k) K = cand;
+    }
+    int n_gt = 0;
+#pragma unroll
+    for (int j = 0; j < EJ; j++) n_gt += __popcll(__ballot(valid[j] && key[j] > K));
+    const int need = k - n_gt;
+    const uint64_t below = __lanemask_lt();
+    int ties_before = 0, picked_before = 0;
+#pragma unroll
+    for (int j = 0; j < EJ; j++) {
+        const uint64_t eq = __ballot(valid[j] && key[j] == K);
+        const bool tie = valid[j] && key[j] == K;
+        const int my_tie = ties_before + __popcll(eq & below);
+        const bool sel = valid[j] && (key[j] > K || (tie && my_tie < need));
+        const uint64_t sm = __ballot(sel);
+        if (sel) {
+            const int c = picked_before + __popcll(sm & below);
+            scratch[2 * c] = __builtin_bit_cast(uint32_t, v[j]);
+            scratch[2 * c + 1] = static_cast<uint32_t>(lane + 64 * j);
+        }
+        ties_before += __popcll(eq);
+        picked_before += __popcll(sm);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // lane r < k ranks compacted pick r among the k (descending value, ties to the lower id) and by id, and puts
+    // it at its descending position in the second half of scratch (id in bits 0..15, id rank in 16..31)
+    if (lane < k) {
+        const uint2 mine = make_uint2(scratch[2 * lane], scratch[2 * lane + 1]);
+        const uint32_t mk = order_key(__builtin_bit_cast(float, mine.x));
+        int desc = 0, id_rank = 0;
+        for (int q = 0; q < k; q++) {
+            const uint2 o = make_uint2(scratch[2 * q], scratch[2 * q + 1]);
+            const uint32_t ok = order_key(__builtin_bit_cast(float, o.x));
+            desc += (ok > mk || (ok == mk && o.y < mine.y)) ? 1 : 0;
+            id_rank += o.y < mine.y ? 1 : 0;
+        }
+        scratch[32 + 2 * desc] = mine.x;
+        scratch[32 + 2 * desc + 1] = mine.y | (static_cast<uint32_t>(id_rank) << 16);
+    }
+    __builtin_amdgcn_wave_barrier();
+    int my_id = 0;
+    float my_v = -INFINITY;
+    out_id_rank = 0;
+    if (lane < k) {
+        const uint2 r = make_uint2(scratch[32 + 2 * lane], scratch[32 + 2 * lane + 1]);
+        my_v = __builtin_bit_cast(float, r.x);
+        my_id = static_cast<int>(r.y & 0xFFFFu);
+        out_id_rank = static_cast<int>(r.y >> 16);
+    }
+    const float p = lane < k ? expf(my_v - m) / s : 0.0f;
+    float wsum = 0.0f;
+    for (int r = 0; r < k; r++) {
+        const float pr = __shfl(p, r);
+        wsum = r == 0 ? pr : wsum + pr;
+    }
+    out_id = my_id;
+    out_w = renorm ? p / wsum : p;
+}
+
+// One intermediate row j of a fused [gate | up] matrix (gate row j, up row inter + j) times one token x, one
+// wavefront; every lane returns the two sums.
+template <int TYPE>
+__device__ __forceinline__ void gate_up_row(const uint8_t* __restrict__ w, int j, int inter, int H,
+                                            const float* __restrict__ x, int lane, float& g, float& u) {
+    const int gi = lane >> 3, c = lane & 7;
+    const int nb = H / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const uint8_t* wg = w + static_cast<int64_t>(j) * rs;
+    const uint8_t* wu = w + static_cast<int64_t>(inter + j) * rs;
+    const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
+    float ag = 0.0f, au = 0.0f;
+    for (int kb = gi; kb < nb; kb += 8) {
+        Lane32 lg, lu;
+        decode<TYPE>(wg + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lg);
+        decode<TYPE>(wu + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lu);
+        const float* xt = x + kb * kQK + lo_start;
+        float4 xl[4], xh[4];
+        load_run(xt, xl);
+        load_run(xt + hi_off, xh);
+        const float sxl = sum16(xl), sxh = sum16(xh);
+        ag += lane_dot_s(lg, xl, xh, sxl, sxh);
+        au += lane_dot_s(lu, xl, xh, sxl, sxh);
+    }
+    g = group_sum<64>(ag);
+    u = group_sum<64>(au);
+}
+
+}  // namespace wl

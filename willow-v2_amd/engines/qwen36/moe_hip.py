@@ -1,0 +1,77 @@
+"""Engine.moe on the HIP backend, as a mixin for willow's engines (engines/base.py:445-490).
+
+Put HipMoE ahead of the reference's Engine in an engine's bases and give the engine an HBMExpertStore as its
+`experts`:
+
+    class Qwen35MoEEngineHip(HipMoE, Qwen35MoEEngine): ...
+
+moe(x, layer, residual) keeps the layer API called at engines/qwen36/model.py:22: x [T, hidden] on the engine's
+device in, the same shape and dtype out. It reads the same attributes and weight names as the reference
+(self.prefix, self.top_k, self.norm_topk_prob; <prefix>layers.N.mlp.{gate, shared_expert.{gate,up,down}_proj,
+shared_expert_gate}.weight; engines/base.py:285-286,446,481-485) and runs the router, top-k, grouping, experts and
+combine on the GPU in one call: no `selected.cpu()` wait per layer (engines/base.py:456-460), no guess of the next
+layer's experts (nothing to prefetch), no per-expert launches.
+
+Shared expert: when its three matrices are GGMLWeight (kept quantized), they run inside the fused kernel; when
+they are dense tensors (the reference's loader dequantizes them to bf16, engines/qwen36/loader.py:224), the
+routed part runs fused and the shared expert is added with the reference's own formula (engines/base.py:104-107).
+Arithmetic is fp32 inside the kernel; the result is cast back to x's dtype.
+"""
+import torch
+import torch.nn.functional as F
+
+from gguf.hip import GGMLWeight
+
+
+def dense_shared_expert(x, gate_w, up_w, down_w, shared_gate_w):
+    """engines/base.py:104-107."""
+    h = F.linear(F.silu(F.linear(x, gate_w)) * F.linear(x, up_w), down_w)
+    return torch.sigmoid(F.linear(x, shared_gate_w)) * h
+
+
+class HipMoE:
+    """Mixin replacing Engine.moe with the fused device-side MoE layer."""
+
+    def hip_layer(self, layer: int):
+        """(MoELayer, dense shared-expert weights or None), built once per layer from the engine's weights."""
+        cache = self.__dict__.setdefault("_hip_moe_layers", {})
+        if layer in cache:
+            return cache[layer]
+        p = f"{self.prefix}layers.{layer}.mlp"
+        device = self.experts.device
+        router = self.weights[p + ".gate.weight"].to(device=device, dtype=torch.float32).contiguous()
+        bias = self.weights.get(p + ".gate.bias")
+        if bias is not None:
+            bias = bias.to(device=device, dtype=torch.float32).contiguous()
+        sp = p + ".shared_expert"
+        names = (sp + ".gate_proj.weight", sp + ".up_proj.weight", sp + ".down_proj.weight")
+        shared = {}
+        dense = None
+        if all(n in self.weights for n in names):
+            gate_w, up_w, down_w = (self.weights[n] for n in names)
+            gate_g = self.weights.get(p + ".shared_expert_gate.weight")
+            quantized = (isinstance(gate_w, GGMLWeight) and isinstance(up_w, GGMLWeight)
+                         and isinstance(down_w, GGMLWeight) and gate_w.type_name == up_w.type_name)
+            if quantized:
+                for w in (gate_w, up_w, down_w):
+                    w.to_gpu()
+                # fused [gate | up] bytes, as the expert pack fuses them (gguf/compiler.py:69-88)
+                shared = dict(shared_gate_up=torch.cat((gate_w.raw.reshape(-1), up_w.raw.reshape(-1))).to(device),
+                              shared_down=down_w.raw.reshape(-1).to(device), shared_inter=gate_w.shape[0],
+                              shared_gate_up_type=gate_w.type_name, shared_down_type=down_w.type_name,
+                              shared_gate=None if gate_g is None else
+                              gate_g.to(device=device, dtype=torch.float32).reshape(-1).contiguous())
+            else:
+                dense = (gate_w, up_w, down_w, gate_g)
+        view = self.experts.layer_view(layer, router, self.top_k, self.norm_topk_prob, router_bias=bias, **shared)
+        cache[layer] = (view, dense)
+        return cache[layer]
+
+    def moe(self, x: torch.Tensor, layer: int, residual: torch.Tensor = None) -> torch.Tensor:
+        view, dense = self.hip_layer(layer)
+        flat = x.reshape(-1, x.shape[-1])
+        out = view(flat.to(view.device))
+        if dense is not None:
+            gate_w, up_w, down_w, gate_g = dense
+            out = out + dense_shared_expert(flat.to(gate_w.dtype), gate_w, up_w, down_w, gate_g).float()
+        return out.to(device=x.device, dtype=x.dtype).view_as(x)

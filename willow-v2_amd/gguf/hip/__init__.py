@@ -20,6 +20,7 @@ BLOCK_SIZES = {"Q4_K": (256, 144), "Q6_K": (256, 210)}  # gguf/reader.py:25,27
 MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many tokens (gguf/metal.py:20)
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
+MOE_NO_FUSED = 1
 
 LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwillow_hip.so")
 
@@ -41,7 +42,7 @@ class WlMoeLayer(ctypes.Structure):
         ("gate_up_type", ctypes.c_int32), ("down_type", ctypes.c_int32), ("shared_gate_up_type", ctypes.c_int32),
         ("shared_down_type", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
         ("shared_inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("top_k", ctypes.c_int32),
-        ("norm_topk_prob", ctypes.c_int32),
+        ("norm_topk_prob", ctypes.c_int32), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
 
 
@@ -74,6 +75,8 @@ def library() -> ctypes.CDLL:
     lib.wl_moe_layer_profile.argtypes = [layer_p, vp, i64, vp, vp, vp, vp, ctypes.c_size_t, vp,
                                          ctypes.POINTER(ctypes.c_void_p)]
     lib.wl_moe_stage_count.argtypes, lib.wl_moe_stage_count.restype = [], c_int
+    lib.wl_moe_plan.argtypes, lib.wl_moe_plan.restype = [layer_p, i64], c_int
+    lib.wl_moe_workspace_init.argtypes, lib.wl_moe_workspace_init.restype = [vp, ctypes.c_size_t, vp], c_int
     lib.wl_moe_stage_name.argtypes, lib.wl_moe_stage_name.restype = [c_int], ctypes.c_char_p
     for name in ("wl_dequant", "wl_gemv", "wl_gemv_batch", "wl_gemv_combine", "wl_moe_check", "wl_moe_route",
                  "wl_moe_layer", "wl_moe_layer_profile"):

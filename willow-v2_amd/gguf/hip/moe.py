@@ -6,7 +6,7 @@ import ctypes
 
 import torch
 
-from . import (TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
+from . import (MOE_NO_FUSED, TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
 
 
 def _ptr(t):
@@ -25,7 +25,7 @@ class MoELayer:
     def __init__(self, *, gate_up, down, router, hidden: int, inter: int, n_experts: int, top_k: int,
                  norm_topk_prob: bool = True, gate_up_type: str = "Q4_K", down_type: str = "Q6_K",
                  router_bias=None, shared_gate_up=None, shared_down=None, shared_gate=None, shared_inter=None,
-                 shared_gate_up_type=None, shared_down_type=None):
+                 shared_gate_up_type=None, shared_down_type=None, fused: bool = True):
         for name, t in (("gate_up", gate_up), ("down", down), ("router", router)):
             _on_gpu(t, name)
         if router.dtype != torch.float32:
@@ -61,11 +61,12 @@ class MoELayer:
         s.shared_down_type = TYPE_IDS.get(self.shared_down_type, -1)
         s.hidden, s.inter, s.shared_inter = hidden, inter, self.shared_inter
         s.n_experts, s.top_k, s.norm_topk_prob = n_experts, top_k, int(self.norm_topk_prob)
+        s.flags = 0 if fused else MOE_NO_FUSED
         self.struct = s
         check(library().wl_moe_check(ctypes.byref(s)))
 
     @classmethod
-    def from_host(cls, lw: dict, device="cuda"):
+    def from_host(cls, lw: dict, device="cuda", fused: bool = True):
         """From a layer dict of numpy arrays (gguf.synth.moe_layer's layout), copied to the GPU."""
         def dev(a):
             return None if a is None else torch.from_numpy(a).to(device)
@@ -76,15 +77,20 @@ class MoELayer:
                    gate_up_type=lw["gate_up_type"], down_type=lw["down_type"],
                    shared_gate_up=dev(lw.get("shared_gate_up")), shared_down=dev(lw.get("shared_down")),
                    shared_gate=dev(lw.get("shared_gate")), shared_inter=lw.get("shared_inter"),
-                   shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"))
+                   shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"),
+                   fused=fused)
 
     def workspace_bytes(self, tokens: int) -> int:
         return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
 
+    def plan(self, tokens: int) -> str:
+        """'fused' (one persistent kernel) or 'multi' (six stages) for this many tokens."""
+        return {1: "fused", 0: "multi"}[library().wl_moe_plan(ctypes.byref(self.struct), tokens)]
+
     def workspace(self, tokens: int) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
         if self._ws is None or self._ws.numel() < need:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            self._ws = new_workspace(need, self.device)
         return self._ws
 
     def __call__(self, x: torch.Tensor, out: torch.Tensor = None, ids: torch.Tensor = None,
@@ -114,6 +120,13 @@ class MoELayer:
         check(library().wl_moe_route(ctypes.byref(self.struct), xf.data_ptr(), tokens, logits.data_ptr(),
                                      ids.data_ptr(), weights.data_ptr(), _ptr(sg), _stream(self.device)))
         return weights, ids, sg
+
+
+def new_workspace(nbytes: int, device) -> torch.Tensor:
+    """A device workspace with its grid-barrier words zeroed (wl_moe_workspace_init), ready for any layer."""
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+    check(library().wl_moe_workspace_init(ws.data_ptr(), ws.numel(), _stream(ws.device)))
+    return ws
 
 
 def moe_layer(x: torch.Tensor, layer: MoELayer) -> torch.Tensor:
