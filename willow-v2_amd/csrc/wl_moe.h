@@ -17,12 +17,18 @@ constexpr int kSortChunk = 256;    // grouping: tokens per bitmap chunk
 constexpr int kSortWords = kSortChunk / 32;
 constexpr int64_t kMaxTokens = 1 << 20;
 constexpr int kMoeStages = 6;  // router, topk, sort, gate_up, down, combine
-constexpr int kFusedMaxK = 8;     // fused decode kernel: most experts per token
-constexpr int kFusedMaxG = 512;   // fused decode kernel: most workgroups (one per CU)
-constexpr int kFlagStride = 32;   // fused decode kernel: words between workgroup flags (one 128-byte line each)
-// fused decode kernel: synchronization words at the start of the workspace (release word, one flag line per
-// workgroup, the routing)
-constexpr int kSyncWords = kFlagStride * (1 + kFusedMaxG) + 2 * kFusedMaxK + 1;
+// fused decode kernel limits
+constexpr int kFusedMaxK = 8;         // experts per token
+constexpr int kFusedMaxE = 256;       // experts
+constexpr int kFusedMaxInter = 1024;  // expert width
+constexpr int kFusedMaxG = 512;       // workgroups (one per CU)
+constexpr int kFlagStride = 32;       // words between workgroups' epoch counters (one 128-byte line each)
+// fused decode kernel: its words at the start of the workspace: epoch counters, then the tagged 64-bit values
+// that cross workgroups (logits [E+1], shared-expert SwiGLU output [I], routed SwiGLU outputs [k, I])
+constexpr int kTagLogits = kFlagStride * kFusedMaxG;
+constexpr int kTagHsh = kTagLogits + 2 * (kFusedMaxE + 16);
+constexpr int kTagH = kTagHsh + 2 * kFusedMaxInter;
+constexpr int kSyncWords = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
 
 struct ExpertArgs {
     const uint8_t* gate_up;

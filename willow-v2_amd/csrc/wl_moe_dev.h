@@ -34,16 +34,18 @@ __device__ __forceinline__ float router_row(const float* __restrict__ x, const f
             }
         }
     }
+    // gather the half's 32 partials of each j first (independent shuffles), then add them in segment order
     float total = 0.0f;
 #pragma unroll
     for (int j = 0; j < kRouterMaxJ; j++) {
         if (32 * j < nseg) {
+            float parts[32];
+#pragma unroll
+            for (int sl = 0; sl < 32; sl++) parts[sl] = __shfl(p[j], src_base + sl);
+#pragma unroll
             for (int sl = 0; sl < 32; sl++) {
                 const int s = sl + 32 * j;
-                if (s < nseg) {
-                    const float v = __shfl(p[j], src_base + sl);
-                    total = s == 0 ? v : __fadd_rn(total, v);
-                }
+                if (s < nseg) total = s == 0 ? parts[sl] : __fadd_rn(total, parts[sl]);
             }
         }
     }
