@@ -99,6 +99,8 @@ typedef struct WlMoeLayer {
 } WlMoeLayer;
 
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */
+#define WL_MOE_NO_MFMA 2         /* flags: never take the bf16 MFMA prefill path (fp32 GEMV path instead) */
+#define WL_MOE_FORCE_MFMA 4      /* flags: take the MFMA prefill path at any token count (testing) */
 
 /* Checks a layer description without touching device memory; 0 or a WL_E* code. */
 int wl_moe_check(const WlMoeLayer* layer);

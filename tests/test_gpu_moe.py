@@ -57,7 +57,7 @@ def test_fused_matches_multi_kernel(hip, c2, layer_c2):
     """Batch-1 decode runs as one fused persistent kernel; it must give the multi-kernel path's routing bits and
     its outputs up to the compiler's multiply-add contraction in the combine (~1e-6)."""
     multi = hip.MoELayer.from_host(layer_c2, fused=False)
-    assert c2.plan(1) == "fused" and multi.plan(1) == "multi" and c2.plan(2) == "multi"
+    assert c2.plan(1) == "fused" and multi.plan(1) == "gemv" and c2.plan(2) == "gemv" and c2.plan(600) == "mfma"
     for seed in range(5):
         x = synth.tokens(200 + seed, 1)
         y_f, ids_f, w_f = run_layer(hip, c2, x)
@@ -135,3 +135,40 @@ def test_layer_variants(hip, variant):
     layer = hip.MoELayer.from_host(lw)
     for T in (1, 5):
         check_layer(hip, layer, lw, synth.tokens(51 + T, T, kw["hidden"]), f"{variant}")
+
+
+def check_prefill(hip, layer, lw, x, label, tol=TOL):
+    """The MFMA path against the oracle with the same bf16 roundings (x, dequantized weights and the SwiGLU
+    output to bf16; fp32 products and sums), and against the all-fp32 oracle within bf16 accuracy."""
+    print(f"[prefill] {label}: T={x.shape[0]}", flush=True)
+    y, ids, wts = run_layer(hip, layer, x)
+    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, bf16_operands=True, return_routing=True)
+    np.testing.assert_array_equal(ids, ids_ref)
+    np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
+    err = moe_ref.rel_err(y, y_b)
+    err32 = moe_ref.rel_err(y, moe_ref.layer(x, lw))
+    print(f"[prefill] {label}: rel err {err:.2e} vs bf16-operand oracle, {err32:.2e} vs fp32 oracle", flush=True)
+    assert err < tol
+    assert err32 < 2e-2
+    return err
+
+
+def test_prefill_mfma_c2(hip, c2, layer_c2):
+    """600 tokens through the full layer: tiled router, grouped bf16 MFMA GEMMs for ~19 tokens per expert."""
+    assert c2.plan(600) == "mfma"
+    check_prefill(hip, c2, layer_c2, synth.tokens(600, 600), "c2 T=600")
+
+
+@pytest.mark.parametrize("variant", ["base", "q4k_down", "no_shared", "inter_256", "partial_tiles"])
+def test_prefill_mfma_variants(hip, variant):
+    kw = dict(hidden=1024, inter=512, shared_inter=512, experts=16, top_k=4)
+    if variant == "q4k_down":
+        kw["down_type"] = "Q4_K"
+    if variant == "inter_256":
+        kw.update(inter=256, shared_inter=256)
+    lw = synth.moe_layer(70, **kw)
+    if variant == "no_shared":
+        lw["shared_gate_up"] = lw["shared_down"] = lw["shared_gate"] = None
+    layer = hip.MoELayer.from_host(lw, mfma="always")
+    T = 37 if variant == "partial_tiles" else 300  # 300 * 4 / 16 = 75 tokens per expert on average
+    check_prefill(hip, layer, lw, synth.tokens(71, T, kw["hidden"]), variant)

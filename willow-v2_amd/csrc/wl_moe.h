@@ -49,6 +49,28 @@ struct ExpertArgs {
     float* o_sh;
 };
 
+constexpr int kTileTokens = 128;             // prefill: tokens per GEMM tile
+constexpr int kMfmaMinTokensPerExpert = 16;  // prefill path when T * top_k >= this * n_experts
+constexpr int kTiledRouterMinTokens = 32;    // router as a tiled kernel from this many tokens
+
+struct PrefillArgs {
+    const uint8_t* gate_up;
+    int64_t gate_up_stride;
+    const uint8_t* down;
+    int64_t down_stride;
+    const uint8_t* sh_gate_up;
+    const uint8_t* sh_down;
+    const uint16_t* xb;      // [T, H] bf16
+    const int32_t* sorted;   // [T*k] pair id by sorted position
+    const int4* tiles;       // (expert or E for the shared expert, first position / token, count)
+    const int32_t* n_tiles;
+    uint16_t* h16;           // [T*k, inter] bf16 by sorted position
+    uint16_t* h_sh16;        // [T, shared_inter] bf16
+    float* o;                // [T*k, H]
+    float* o_sh;             // [T, H]
+    int H, inter, sh_inter, E, k;
+};
+
 struct Workspace {
     uint32_t* sync;     // [kSyncWords] grid-barrier words of the fused kernel (zeroed once, left zeroed)
     float* logits;      // [T, E + 1]
@@ -66,6 +88,12 @@ struct Workspace {
     float* o;           // [T*k, hidden]  by sorted position
     float* h_sh;        // [T, shared_inter]
     float* o_sh;        // [T, hidden]
+    // prefill (MFMA) path only
+    uint16_t* xb;       // [T, hidden] bf16
+    int4* tiles;        // [max_tiles]
+    int32_t* n_tiles;   // [1]
+    uint16_t* h16;      // [T*k, inter] bf16
+    uint16_t* h_sh16;   // [T, shared_inter] bf16
     size_t bytes;
 };
 
@@ -75,5 +103,9 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T);
 int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,
                  hipStream_t s);
 int zero_sync(void* workspace, hipStream_t s);
+bool prefill_eligible(const WlMoeLayer& L, int64_t T);
+int max_tiles(const WlMoeLayer& L, int64_t T);
+int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s);
+int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s);
 
 }  // namespace wl

@@ -516,6 +516,12 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.o = static_cast<float*>(take(sizeof(float) * P * L.hidden));
     w.h_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.shared_inter : 0));
     w.o_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.hidden : 0));
+    const bool mfma = prefill_eligible(L, T);
+    w.xb = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * T * L.hidden : 0));
+    w.tiles = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T) : 0));
+    w.n_tiles = static_cast<int32_t*>(take(mfma ? sizeof(int32_t) : 0));
+    w.h16 = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * P * L.inter : 0));
+    w.h_sh16 = static_cast<uint16_t*>(take(mfma && shared ? sizeof(uint16_t) * T * L.shared_inter : 0));
     w.bytes = off;
     return w;
 }
@@ -641,6 +647,53 @@ static void launch_down(int type, const ExpertArgs& a, int inter, int slots, hip
         launch_down_t<WL_TYPE_Q6_K>(a, inter, slots, s);
 }
 
+// The fp32 expert stages (gate_up + SwiGLU, down) for few tokens per expert.
+template <typename Mark>
+static int launch_gemv_experts(const WlMoeLayer& L, const float* x, int64_t tokens, const Workspace& w,
+                               hipStream_t s, Mark mark) {
+    const bool shared = L.shared_gate_up != nullptr;
+    ExpertArgs a{};
+    a.gate_up = static_cast<const uint8_t*>(L.gate_up);
+    a.gate_up_stride = L.gate_up_stride;
+    a.down = static_cast<const uint8_t*>(L.down);
+    a.down_stride = L.down_stride;
+    a.sh_gate_up = static_cast<const uint8_t*>(L.shared_gate_up);
+    a.sh_down = static_cast<const uint8_t*>(L.shared_down);
+    a.x = x;
+    a.T = static_cast<int>(tokens);
+    a.H = L.hidden;
+    a.inter = L.inter;
+    a.sh_inter = shared ? L.shared_inter : 0;
+    a.k = L.top_k;
+    a.offsets = w.offsets;
+    a.active = w.active;
+    a.sorted = w.sorted;
+    a.h = w.h;
+    a.h_sh = w.h_sh;
+    a.o = w.o;
+    a.o_sh = w.o_sh;
+    const int max_active = static_cast<int>(tokens * L.top_k < L.n_experts ? tokens * L.top_k : L.n_experts);
+
+    // gate_up + SwiGLU: routed experts, then (same kernel when the types agree) the shared expert
+    const bool fuse_gu = shared && L.shared_gate_up_type == L.gate_up_type && L.shared_inter == L.inter;
+    a.n_routed = max_active;
+    launch_gate_up(L.gate_up_type, a, L.inter, max_active + (fuse_gu ? 1 : 0), s);
+    if (shared && !fuse_gu) {
+        ExpertArgs b = a;
+        b.n_routed = 0;
+        launch_gate_up(L.shared_gate_up_type, b, L.shared_inter, 1, s);
+    }
+    const bool fuse_dn = shared && L.shared_down_type == L.down_type && L.shared_inter == L.inter;
+    mark(4);
+    launch_down(L.down_type, a, L.inter, max_active + (fuse_dn ? 1 : 0), s);
+    if (shared && !fuse_dn) {
+        ExpertArgs b = a;
+        b.n_routed = 0;
+        launch_down(L.shared_down_type, b, L.shared_inter, 1, s);
+    }
+    return launch_status();
+}
+
 }  // namespace wl
 
 using namespace wl;
@@ -687,6 +740,7 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
     return launch_topk(*layer, logits, tokens, ids, weights, nullptr, s);
 }
 
+
 static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
                      float* weights, void* workspace, size_t workspace_bytes, void* stream, void* const* events) {
     int rc = check_layer(layer);
@@ -717,7 +771,8 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
     auto mark = record;
     mark(0);
-    rc = launch_router(L, x, tokens, w.logits, sg, s);
+    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, s)
+                                         : launch_router(L, x, tokens, w.logits, sg, s);
     if (rc) return rc;
     mark(1);
     rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
@@ -726,48 +781,14 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     rc = launch_sort(L, w, w.ids, tokens, s);
     if (rc) return rc;
     mark(3);
-
-    ExpertArgs a{};
-    a.gate_up = static_cast<const uint8_t*>(L.gate_up);
-    a.gate_up_stride = L.gate_up_stride;
-    a.down = static_cast<const uint8_t*>(L.down);
-    a.down_stride = L.down_stride;
-    a.sh_gate_up = static_cast<const uint8_t*>(L.shared_gate_up);
-    a.sh_down = static_cast<const uint8_t*>(L.shared_down);
-    a.x = x;
-    a.T = static_cast<int>(tokens);
-    a.H = L.hidden;
-    a.inter = L.inter;
-    a.sh_inter = shared ? L.shared_inter : 0;
-    a.k = L.top_k;
-    a.offsets = w.offsets;
-    a.active = w.active;
-    a.sorted = w.sorted;
-    a.h = w.h;
-    a.h_sh = w.h_sh;
-    a.o = w.o;
-    a.o_sh = w.o_sh;
-    const int max_active = static_cast<int>(tokens * L.top_k < L.n_experts ? tokens * L.top_k : L.n_experts);
-
-    // gate_up + SwiGLU: routed experts, then (same kernel when the types agree) the shared expert
-    const bool fuse_gu = shared && L.shared_gate_up_type == L.gate_up_type && L.shared_inter == L.inter;
-    a.n_routed = max_active;
-    launch_gate_up(L.gate_up_type, a, L.inter, max_active + (fuse_gu ? 1 : 0), s);
-    if (shared && !fuse_gu) {
-        ExpertArgs b = a;
-        b.n_routed = 0;
-        launch_gate_up(L.shared_gate_up_type, b, L.shared_inter, 1, s);
+    if (prefill_eligible(L, tokens)) {  // bf16 MFMA GEMMs (gate_up + SwiGLU in one stage, down in the next)
+        rc = launch_prefill_experts(L, x, tokens, w, s);
+        if (rc) return rc;
+        mark(4);
+    } else {
+        rc = launch_gemv_experts(L, x, tokens, w, s, mark);
+        if (rc) return rc;
     }
-    const bool fuse_dn = shared && L.shared_down_type == L.down_type && L.shared_inter == L.inter;
-    mark(4);
-    launch_down(L.down_type, a, L.inter, max_active + (fuse_dn ? 1 : 0), s);
-    if (shared && !fuse_dn) {
-        ExpertArgs b = a;
-        b.n_routed = 0;
-        launch_down(L.shared_down_type, b, L.shared_inter, 1, s);
-    }
-    rc = launch_status();
-    if (rc) return rc;
     mark(5);
     const int64_t threads = tokens * (L.hidden / 4);
     k_combine<<<static_cast<int>((threads + 255) / 256), 256, 0, s>>>(
@@ -777,6 +798,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     mark(6);
     return rc;
 }
+
 
 int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
                  void* workspace, size_t workspace_bytes, void* stream) {
@@ -796,7 +818,8 @@ int wl_moe_stage_count(void) { return kMoeStages; }
 
 int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens) {
     if (check_layer(layer) != WL_OK || tokens <= 0) return -1;
-    return fused_eligible(*layer, tokens) ? 1 : 0;
+    if (fused_eligible(*layer, tokens)) return 1;
+    return prefill_eligible(*layer, tokens) ? 2 : 0;
 }
 
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {

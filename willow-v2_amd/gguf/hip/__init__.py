@@ -20,7 +20,7 @@ BLOCK_SIZES = {"Q4_K": (256, 144), "Q6_K": (256, 210)}  # gguf/reader.py:25,27
 MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many tokens (gguf/metal.py:20)
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
-MOE_NO_FUSED = 1
+MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA = 1, 2, 4
 
 LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwillow_hip.so")
 

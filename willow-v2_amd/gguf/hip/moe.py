@@ -6,7 +6,7 @@ import ctypes
 
 import torch
 
-from . import (MOE_NO_FUSED, TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
+from . import (MOE_FORCE_MFMA, MOE_NO_FUSED, MOE_NO_MFMA, TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
 
 
 def _ptr(t):
@@ -25,7 +25,7 @@ class MoELayer:
     def __init__(self, *, gate_up, down, router, hidden: int, inter: int, n_experts: int, top_k: int,
                  norm_topk_prob: bool = True, gate_up_type: str = "Q4_K", down_type: str = "Q6_K",
                  router_bias=None, shared_gate_up=None, shared_down=None, shared_gate=None, shared_inter=None,
-                 shared_gate_up_type=None, shared_down_type=None, fused: bool = True):
+                 shared_gate_up_type=None, shared_down_type=None, fused: bool = True, mfma: str = "auto"):
         for name, t in (("gate_up", gate_up), ("down", down), ("router", router)):
             _on_gpu(t, name)
         if router.dtype != torch.float32:
@@ -61,12 +61,14 @@ class MoELayer:
         s.shared_down_type = TYPE_IDS.get(self.shared_down_type, -1)
         s.hidden, s.inter, s.shared_inter = hidden, inter, self.shared_inter
         s.n_experts, s.top_k, s.norm_topk_prob = n_experts, top_k, int(self.norm_topk_prob)
-        s.flags = 0 if fused else MOE_NO_FUSED
+        if mfma not in ("auto", "never", "always"):
+            raise ValueError("mfma must be 'auto', 'never' or 'always'")
+        s.flags = (0 if fused else MOE_NO_FUSED) | {"auto": 0, "never": MOE_NO_MFMA, "always": MOE_FORCE_MFMA}[mfma]
         self.struct = s
         check(library().wl_moe_check(ctypes.byref(s)))
 
     @classmethod
-    def from_host(cls, lw: dict, device="cuda", fused: bool = True):
+    def from_host(cls, lw: dict, device="cuda", fused: bool = True, mfma: str = "auto"):
         """From a layer dict of numpy arrays (gguf.synth.moe_layer's layout), copied to the GPU."""
         def dev(a):
             return None if a is None else torch.from_numpy(a).to(device)
@@ -78,14 +80,15 @@ class MoELayer:
                    shared_gate_up=dev(lw.get("shared_gate_up")), shared_down=dev(lw.get("shared_down")),
                    shared_gate=dev(lw.get("shared_gate")), shared_inter=lw.get("shared_inter"),
                    shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"),
-                   fused=fused)
+                   fused=fused, mfma=mfma)
 
     def workspace_bytes(self, tokens: int) -> int:
         return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
 
     def plan(self, tokens: int) -> str:
-        """'fused' (one persistent kernel) or 'multi' (six stages) for this many tokens."""
-        return {1: "fused", 0: "multi"}[library().wl_moe_plan(ctypes.byref(self.struct), tokens)]
+        """'fused' (one persistent kernel), 'mfma' (bf16 MFMA expert GEMMs) or 'gemv' (fp32 expert GEMVs) for this
+        many tokens."""
+        return {1: "fused", 2: "mfma", 0: "gemv"}[library().wl_moe_plan(ctypes.byref(self.struct), tokens)]
 
     def workspace(self, tokens: int) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
