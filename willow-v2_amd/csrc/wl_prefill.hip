@@ -132,29 +132,64 @@ __global__ __launch_bounds__(256) void k_to_bf16(const float* __restrict__ x, ui
 
 // Tiles of up to kTileTokens tokens: each routed expert's sorted positions, then the shared expert's tokens
 // (expert id E). tiles[i] = (expert, first position or token, count); n_tiles[0] = how many.
-__global__ void k_tiles(const int32_t* __restrict__ offsets, int E, int T, int with_shared, int4* __restrict__ tiles,
-                        int32_t* __restrict__ n_tiles) {
-    if (threadIdx.x != 0) return;
-    int n = 0;
-    for (int e = 0; e < E; e++) {
+// One workgroup of 256 threads, thread i owning experts 4i .. 4i + 3 (E <= 1024): tile counts, an exclusive scan
+// of them across the workgroup, then each thread writes its experts' tiles in expert order.
+__global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offsets, int E, int T, int with_shared,
+                                               int4* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+    __shared__ int scan[2][256];
+    const int tid = threadIdx.x;
+    int cnt[4], mine = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = 4 * tid + i;
+        cnt[i] = e < E ? (offsets[e + 1] - offsets[e] + kTileTokens - 1) / kTileTokens : 0;
+        mine += cnt[i];
+    }
+    int cur = 0;
+    scan[0][tid] = mine;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const int v = scan[cur][tid] + (tid >= off ? scan[cur][tid - off] : 0);
+        scan[cur ^ 1][tid] = v;
+        cur ^= 1;
+        __syncthreads();
+    }
+    int n = scan[cur][tid] - mine;  // tiles before this thread's experts
+    const int total = scan[cur][255];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = 4 * tid + i;
+        if (e >= E) break;
         const int b = offsets[e], c = offsets[e + 1] - b;
         for (int p = 0; p < c; p += kTileTokens) tiles[n++] = make_int4(e, b + p, min(kTileTokens, c - p), 0);
     }
+    int m = total;
     if (with_shared)
-        for (int p = 0; p < T; p += kTileTokens) tiles[n++] = make_int4(E, p, min(kTileTokens, T - p), 0);
-    n_tiles[0] = n;
+        for (int p = tid * kTileTokens; p < T; p += 256 * kTileTokens)
+            tiles[total + p / kTileTokens] = make_int4(E, p, min(kTileTokens, T - p), 0);
+    if (with_shared) m += (T + kTileTokens - 1) / kTileTokens;
+    if (tid == 0) n_tiles[0] = m;
 }
 
 // Stages a tile's activations [count tokens][kBK values from k0] (bf16) into LDS; rows past count are zero.
-// src_row(t) gives the row of token t of the tile in `src` ([*, ld] bf16).
-template <typename RowFn>
+// rows[t] is the row of token t of the tile in `src` ([*, ld] bf16). All of a thread's loads are issued before
+// any is stored (a blockDim of 256 gives 16 each).
 __device__ __forceinline__ void stage_tile(uint16_t* lds, const uint16_t* __restrict__ src, int64_t ld, int k0,
-                                           int count, RowFn src_row) {
-    for (int i = threadIdx.x; i < kTileTokens * (kBK / 8); i += blockDim.x) {
+                                           int count, const int* rows) {
+    constexpr int kPer = kTileTokens * (kBK / 8) / 256;
+    uint4 v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int i = threadIdx.x + 256 * u;
         const int t = i / (kBK / 8), c8 = (i % (kBK / 8)) * 8;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (t < count) v = *reinterpret_cast<const uint4*>(src + src_row(t) * ld + k0 + c8);
-        *reinterpret_cast<uint4*>(lds + t * kLdsRow + c8) = v;
+        v[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (t < count) v[u] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(rows[t]) * ld + k0 + c8);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int i = threadIdx.x + 256 * u;
+        const int t = i / (kBK / 8), c8 = (i % (kBK / 8)) * 8;
+        *reinterpret_cast<uint4*>(lds + t * kLdsRow + c8) = v[u];
     }
 }
 
@@ -172,21 +207,32 @@ __device__ __forceinline__ void fetch_q4k(const uint8_t* __restrict__ blk, int q
     for (int m = 0; m < 4; m++) s.qs[m] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * m + 8 * q);
 }
 
-__device__ __forceinline__ bf16x8 fragment_q4k(const Q4KRowState& s, int kk) {
+// v & 0x0F0F0F0F as an opaque value, so the byte conversions below stay single v_cvt_f32_ubyteN instructions
+__device__ __forceinline__ uint32_t nibbles(uint32_t v) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// 4 bytes of w (values 0..255) as bf16 of a * q + b, packed two per dword
+__device__ __forceinline__ void affine4(uint32_t w, float a, float b, uint32_t& p0, uint32_t& p1) {
+    p0 = pack2(__builtin_fmaf(a, ubyte(w, 0), b), __builtin_fmaf(a, ubyte(w, 1), b));
+    p1 = pack2(__builtin_fmaf(a, ubyte(w, 2), b), __builtin_fmaf(a, ubyte(w, 3), b));
+}
+
+template <int KK>
+__device__ __forceinline__ bf16x8 fragment_q4k(const Q4KRowState& s) {
     const float d = half_to_float(s.hd.x), dmin = half_to_float(s.hd.x >> 16);
     uint32_t sc, m;
-    q4k_scale_min(kk, s.hd.y, s.hd.z, s.hd.w, sc, m);
+    q4k_scale_min(KK, s.hd.y, s.hd.z, s.hd.w, sc, m);
     const float a = d * static_cast<float>(sc), b = -(dmin * static_cast<float>(m));
-    const uint2 raw = s.qs[kk >> 1];
-    const uint32_t sh = 4 * (kk & 1);
-    const uint32_t lo = (raw.x >> sh) & 0x0F0F0F0Fu, hi = (raw.y >> sh) & 0x0F0F0F0Fu;
-    bf16x8 v;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[i] = static_cast<__bf16>(__builtin_fmaf(a, ubyte(lo, i), b));
-        v[4 + i] = static_cast<__bf16>(__builtin_fmaf(a, ubyte(hi, i), b));
-    }
-    return v;
+    const uint2 raw = s.qs[KK >> 1];
+    constexpr uint32_t sh = 4 * (KK & 1);
+    const uint32_t lo = nibbles(raw.x >> sh), hi = nibbles(raw.y >> sh);
+    uint4 p;
+    affine4(lo, a, b, p.x, p.y);
+    affine4(hi, a, b, p.z, p.w);
+    return __builtin_bit_cast(bf16x8, p);
 }
 
 struct Q6KRowState {
@@ -213,24 +259,25 @@ __device__ __forceinline__ void fetch_q6k(const uint8_t* __restrict__ blk, int q
     s.d = half_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
 }
 
-__device__ __forceinline__ bf16x8 fragment_q6k(const Q6KRowState& s, int kk, int q) {
-    // values e = 32 kk + 8 q + i: half h = kk / 4, quarter t = kk % 4, scale index e / 16 = 2 kk + q / 2
-    const int h = kk >> 2, t = kk & 3;
+template <int KK>
+__device__ __forceinline__ bf16x8 fragment_q6k(const Q6KRowState& s, int q) {
+    // values e = 32 kk + 8 q + i: half h = kk / 4, quarter t = kk % 4, scale index e / 16 = 2 kk + q / 2; the
+    // scale word holds indices 4w .. 4w + 3 with w = kk / 2, and q / 2 picks one of the two in this kk's half
+    constexpr int h = KK >> 2, t = KK & 3;
     const uint2 l4 = s.ql[2 * h + (t & 1)];
     const uint2 h2 = s.qh[h];
-    const uint32_t lsh = 4 * (t >> 1), hsh = 2 * t;
-    const int si = 2 * kk + (q >> 1);
-    const uint32_t scw = si < 4 ? s.sc.x : si < 8 ? s.sc.y : si < 12 ? s.sc.z : s.sc.w;
-    const float a = s.d * static_cast<float>(static_cast<int8_t>((scw >> (8 * (si & 3))) & 0xFFu));
-    const uint32_t v0 = ((l4.x >> lsh) & 0x0F0F0F0Fu) | (((h2.x >> hsh) & 0x03030303u) << 4);
-    const uint32_t v1 = ((l4.y >> lsh) & 0x0F0F0F0Fu) | (((h2.y >> hsh) & 0x03030303u) << 4);
-    bf16x8 v;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[i] = static_cast<__bf16>(a * static_cast<float>(static_cast<int>((v0 >> (8 * i)) & 0xFFu) - 32));
-        v[4 + i] = static_cast<__bf16>(a * static_cast<float>(static_cast<int>((v1 >> (8 * i)) & 0xFFu) - 32));
-    }
-    return v;
+    constexpr uint32_t lsh = 4 * (t >> 1), hsh = 2 * t;
+    const uint32_t scw = (KK >> 1) == 0 ? s.sc.x : (KK >> 1) == 1 ? s.sc.y : (KK >> 1) == 2 ? s.sc.z : s.sc.w;
+    const uint32_t sbyte = (scw >> (8 * (2 * (KK & 1) + (q >> 1)))) & 0xFFu;
+    const float a = s.d * static_cast<float>(static_cast<int8_t>(sbyte));
+    const float b = -32.0f * a;  // exact: a has at most 18 significant bits
+    const uint32_t v0 = nibbles(l4.x >> lsh) | ((nibbles(h2.x >> hsh) & 0x03030303u) << 4);
+    const uint32_t v1 = nibbles(l4.y >> lsh) | ((nibbles(h2.y >> hsh) & 0x03030303u) << 4);
+    // a * (q - 32) == fma(a, q, -32 a): the product a * q is exact, so both round the same sum once
+    uint4 p;
+    affine4(v0, a, b, p.x, p.y);
+    affine4(v1, a, b, p.z, p.w);
+    return __builtin_bit_cast(bf16x8, p);
 }
 
 template <int TYPE>
@@ -239,52 +286,74 @@ template <>
 struct RowState<WL_TYPE_Q4_K> {
     Q4KRowState s;
     __device__ __forceinline__ void fetch(const uint8_t* blk, int q) { fetch_q4k(blk, q, s); }
-    __device__ __forceinline__ bf16x8 frag(int kk, int) const { return fragment_q4k(s, kk); }
+    template <int KK>
+    __device__ __forceinline__ bf16x8 frag(int) const { return fragment_q4k<KK>(s); }
 };
 template <>
 struct RowState<WL_TYPE_Q6_K> {
     Q6KRowState s;
     __device__ __forceinline__ void fetch(const uint8_t* blk, int q) { fetch_q6k(blk, q, s); }
-    __device__ __forceinline__ bf16x8 frag(int kk, int q) const { return fragment_q6k(s, kk, q); }
+    template <int KK>
+    __device__ __forceinline__ bf16x8 frag(int q) const { return fragment_q6k<KK>(s, q); }
 };
 
+// One 32-value step of the K chunk: 4 A-fragments decoded from the row states, then the token tiles in groups of 4
+// (all 4 B-fragments read from LDS before their 16 MFMAs); groups past the tile's tokens are skipped.
+template <int TYPE, int KK>
+__device__ __forceinline__ void gemm_step(const uint16_t* lds, const RowState<TYPE> (&rs)[4], floatx4 (&acc)[4][8],
+                                          int ngroups, int lr, int q) {
+    bf16x8 af[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) af[r] = rs[r].template frag<KK>(q);
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+        if (g < ngroups) {
+            bf16x8 bf[4];
+#pragma unroll
+            for (int n = 0; n < 4; n++)
+                bf[n] = *reinterpret_cast<const bf16x8*>(lds + (16 * (4 * g + n) + lr) * kLdsRow + 32 * KK + 8 * q);
+#pragma unroll
+            for (int n = 0; n < 4; n++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[r][4 * g + n] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[r], bf[n], acc[r][4 * g + n], 0, 0, 0);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
-// The GEMM core: a workgroup of 4 wavefronts, each owning 4 row tiles of 16 (rows given by row_of(w, r, lr)) and
+// The GEMM core: a workgroup of 4 wavefronts, each owning 4 row tiles of 16 (rows given by row_ptr(r, lr)) and
 // the tile's (up to) 128 tokens as 8 token tiles. For each K chunk of 256 (one block per row) the activations are
-// staged in LDS, every wavefront fetches its rows' blocks, and for each 32-value step decodes 4 A-fragments and
-// runs up to 32 MFMAs (token tiles past `count` are skipped).
+// staged in LDS, every wavefront fetches its rows' blocks, and each of the 8 32-value steps decodes 4 A-fragments
+// and runs up to 32 MFMAs.
 template <int TYPE, typename RowPtr, typename SrcRow>
 __device__ __forceinline__ void gemm_tile(uint16_t* lds, floatx4 (&acc)[4][8], int nblocks, int count,
                                           const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
                                           RowPtr row_ptr) {
+    __shared__ int rows[kTileTokens];
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
-    const int ntt = (count + 15) >> 4;
+    const int ngroups = (count + 63) >> 6;
+    for (int t = threadIdx.x; t < count; t += blockDim.x) rows[t] = static_cast<int>(src_row(t));
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
         for (int n = 0; n < 8; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int kc = 0; kc < nblocks; kc++) {
         __syncthreads();
-        stage_tile(lds, src, ld, kc * kBK, count, src_row);
+        stage_tile(lds, src, ld, kc * kBK, count, rows);
         RowState<TYPE> rs[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) rs[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kc) * BlockInfo<TYPE>::bytes, q);
         __syncthreads();
-#pragma unroll 2
-        for (int kk = 0; kk < kBK / 32; kk++) {
-            bf16x8 af[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) af[r] = rs[r].frag(kk, q);
-#pragma unroll
-            for (int n = 0; n < 8; n++) {
-                if (n < ntt) {
-                    const bf16x8 bf = *reinterpret_cast<const bf16x8*>(lds + (16 * n + lr) * kLdsRow + 32 * kk + 8 * q);
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        acc[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[r], bf, acc[r][n], 0, 0, 0);
-                }
-            }
-        }
+        gemm_step<TYPE, 0>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 1>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 2>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 3>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 4>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 5>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 6>(lds, rs, acc, ngroups, lr, q);
+        gemm_step<TYPE, 7>(lds, rs, acc, ngroups, lr, q);
     }
 }
 
@@ -383,7 +452,7 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     const int64_t n8 = T * L.hidden / 8;
     k_to_bf16<<<static_cast<unsigned>((n8 + 255) / 256), 256, 0, s>>>(x, w.xb, n8);
     const bool shared = L.shared_gate_up != nullptr;
-    k_tiles<<<1, 64, 0, s>>>(w.offsets, L.n_experts, static_cast<int>(T), shared ? 1 : 0, w.tiles, w.n_tiles);
+    k_tiles<<<1, 256, 0, s>>>(w.offsets, L.n_experts, static_cast<int>(T), shared ? 1 : 0, w.tiles, w.n_tiles);
     PrefillArgs a{};
     a.gate_up = static_cast<const uint8_t*>(L.gate_up);
     a.gate_up_stride = L.gate_up_stride;
