@@ -69,6 +69,7 @@ struct PrefillArgs {
     float* o;                // [T*k, H]
     float* o_sh;             // [T, H]
     int H, inter, sh_inter, E, k;
+    int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
 };
 
 struct Workspace {

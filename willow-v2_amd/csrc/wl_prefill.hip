@@ -27,20 +27,24 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 256;              // k per staged chunk: one K-quant block per row
-constexpr int kLdsRow = kBK + 8;      // bf16 per LDS row (16-byte pad: conflict-free B reads)
+constexpr int kTileRowBytes = kBK * 2;                     // one token's chunk in LDS: 512 bytes, 32 slots of 16
+constexpr int kTileBytes = kTileTokens * kTileRowBytes;     // 64 KiB per buffer
 
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even, like Tensor.to(torch.bfloat16)) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{a, b}, bf16x2));
 }
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return bf16_bits(a) | (bf16_bits(b) << 16); }
 
-// 8 bytes from a 2-byte-aligned address (3 aligned dwords, realigned); stays within [p - 2, p + 10).
+// 8 bytes from a 2-byte-aligned address: 3 aligned dwords, realigned. Reads [p & ~3, (p & ~3) + 12), within
+// [p - 2, p + 12); all three loads are unconditional so that no branch splits the wavefront.
 __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
     const uint32_t sh = static_cast<uint32_t>(a & 3u);
-    const uint32_t w0 = q[0], w1 = q[1];
-    const uint32_t w2 = sh ? q[2] : 0u;
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
     return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
 }
 
@@ -171,28 +175,6 @@ __global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offse
     if (tid == 0) n_tiles[0] = m;
 }
 
-// Stages a tile's activations [count tokens][kBK values from k0] (bf16) into LDS; rows past count are zero.
-// rows[t] is the row of token t of the tile in `src` ([*, ld] bf16). All of a thread's loads are issued before
-// any is stored (a blockDim of 256 gives 16 each).
-__device__ __forceinline__ void stage_tile(uint16_t* lds, const uint16_t* __restrict__ src, int64_t ld, int k0,
-                                           int count, const int* rows) {
-    constexpr int kPer = kTileTokens * (kBK / 8) / 256;
-    uint4 v[kPer];
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = threadIdx.x + 256 * u;
-        const int t = i / (kBK / 8), c8 = (i % (kBK / 8)) * 8;
-        v[u] = make_uint4(0u, 0u, 0u, 0u);
-        if (t < count) v[u] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(rows[t]) * ld + k0 + c8);
-    }
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-        const int i = threadIdx.x + 256 * u;
-        const int t = i / (kBK / 8), c8 = (i % (kBK / 8)) * 8;
-        *reinterpret_cast<uint4*>(lds + t * kLdsRow + c8) = v[u];
-    }
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // A-operand decoders: the 8 values k = 32*kk + 8*q + i (i < 8) of one row's K-quant block as bf16, for every kk of
 // the block. The per-block state is fetched once (fetch), then each kk is unpacked (fragment).
@@ -247,13 +229,13 @@ __device__ __forceinline__ void fetch_q6k(const uint8_t* __restrict__ blk, int q
     for (int m = 0; m < 4; m++) s.ql[m] = load8_a2(blk + 64 * (m >> 1) + 32 * (m & 1) + 8 * q);
 #pragma unroll
     for (int h = 0; h < 2; h++) s.qh[h] = load8_a2(blk + 128 + 32 * h + 8 * q);
-    // scales: bytes 192..207 from dwords of their aligned start; the fifth dword (needed only when the block starts
-    // 2 bytes into a dword) ends at byte 210, the block's end
+    // scales: bytes 192..207 from the 4 dwords of their aligned start (bytes 190..205 or 192..207) and, for a block
+    // 2 bytes into a dword, bytes 206..207 as a 16-bit load (the realignment takes only its low half)
     const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 192);
     const uint32_t* p = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
     const uint32_t sh = static_cast<uint32_t>(a & 3u);
     const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3];
-    const uint32_t w4 = sh ? p[4] : 0u;
+    const uint32_t w4 = *reinterpret_cast<const uint16_t*>(blk + 206);
     s.sc = make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
                       __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh));
     s.d = half_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
@@ -297,77 +279,212 @@ struct RowState<WL_TYPE_Q6_K> {
     __device__ __forceinline__ bf16x8 frag(int q) const { return fragment_q6k<KK>(s, q); }
 };
 
-// One 32-value step of the K chunk: 4 A-fragments decoded from the row states, then the token tiles in groups of 4
-// (all 4 B-fragments read from LDS before their 16 MFMAs); groups past the tile's tokens are skipped.
-template <int TYPE, int KK>
-__device__ __forceinline__ void gemm_step(const uint16_t* lds, const RowState<TYPE> (&rs)[4], floatx4 (&acc)[4][8],
-                                          int ngroups, int lr, int q) {
-    bf16x8 af[4];
+// ---------------------------------------------------------------------------------------------------------------
+// LDS tile of one K chunk: [128 tokens][256 values] bf16, 512 bytes per token, no padding; the 16-byte slot holding
+// values 8c .. 8c + 7 of token t is slot c ^ (t & 7) of the token's row, so the 8 tokens lr = 0..7 a B-fragment read
+// serves at once sit in 8 different bank groups.
+//
+// B-fragment (token t = 16 n + lr, values 32 KK + 8 q .. + 7) byte address: 512 t + 16 ((4 KK + q) ^ (lr & 7)).
+// With y = q ^ (lr & 7) = 4 y2 + y01 that is 512 lr + 16 y01 + 64 (KK ^ y2) + 8192 n, and 64 (KK ^ y2) =
+// 64 KK + 64 y2 for even KK, 64 KK - 64 y2 for odd KK: two per-lane bases plus a constant offset per (KK, n).
+struct BAddr {
+    uint32_t even, odd;
+};
+__device__ __forceinline__ BAddr b_addr(int lr, int q) {
+    const int y = q ^ (lr & 7), y2 = y >> 2, base = 512 * lr + 16 * (y & 3);
+    return BAddr{static_cast<uint32_t>(base + 64 * y2), static_cast<uint32_t>(base - 64 * y2)};
+}
+template <int KK>
+__device__ __forceinline__ bf16x8 read_b1(const uint8_t* buf, BAddr ba, int n) {
+    return *reinterpret_cast<const bf16x8*>(buf + ((KK & 1) ? ba.odd : ba.even) + 64 * KK + 8192 * n);
+}
+template <int NT, int KK>
+__device__ __forceinline__ void read_b(const uint8_t* buf, BAddr ba, bf16x8 (&b)[8]) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) af[r] = rs[r].template frag<KK>(q);
+    for (int n = 0; n < NT; n++) b[n] = read_b1<KK>(buf, ba, n);
+}
+
+// Explicit MFMA / VALU interleave through scheduling barriers (the compiler's default order otherwise). Off: it
+// multiplies this file's compile time by ~100.
+constexpr bool kSchedGroups = false;
+
+// One 32-value step, software-pipelined: the MFMAs of step KK (A-fragments `a`, B-fragments `b`) are interleaved
+// with decoding step KK + 1's A-fragments into `an` (from `nx`, the next block's rows, when KK is the chunk's last
+// step) and, as each b[n] has been consumed, reading step KK + 1's b[n] in its place (the last step's successor
+// reads from the other LDS buffer after the barrier), so the decode runs while the matrix core is busy.
+template <int TYPE, int NT, int KK>
+__device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const RowState<TYPE> (&rs)[4],
+                                          const RowState<TYPE> (&nx)[4], floatx4 (&acc)[4][8], const bf16x8 (&a)[4],
+                                          bf16x8 (&b)[8], bf16x8 (&an)[4], int q) {
 #pragma unroll
-    for (int g = 0; g < 2; g++) {
-        if (g < ngroups) {
-            bf16x8 bf[4];
+    for (int r = 0; r < 4; r++) {
+        if constexpr (KK < 7)
+            an[r] = rs[r].template frag<KK + 1>(q);
+        else
+            an[r] = nx[r].template frag<0>(q);
+    }
 #pragma unroll
-            for (int n = 0; n < 4; n++)
-                bf[n] = *reinterpret_cast<const bf16x8*>(lds + (16 * (4 * g + n) + lr) * kLdsRow + 32 * KK + 8 * q);
+    for (int n = 0; n < NT; n++) {
 #pragma unroll
-            for (int n = 0; n < 4; n++)
+        for (int r = 0; r < 4; r++)
+            acc[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r], b[n], acc[r][n], 0, 0, 0);
+        if constexpr (KK < 7) b[n] = read_b1<KK + 1>(buf, ba, n);
+    }
+    if constexpr (kSchedGroups) {
+        // 4 NT MFMAs per step against ~120 VALU instructions of decode
+        constexpr int kValuPer = NT == 8 ? 4 : 8;
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[r][4 * g + n] =
-                        __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[r], bf[n], acc[r][4 * g + n], 0, 0, 0);
+        for (int i = 0; i < 4 * NT; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (KK < 7 && (i & 3) == 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
         }
     }
 }
 
+// Direct global -> LDS staging of a K chunk with gfx950's global_load_lds_dwordx4: one wavefront instruction writes
+// 64 consecutive 16-byte LDS slots (M0 + 16 lane), two token rows. Instruction `it` of wavefront w fills rows
+// 8 it + 2 w + (lane >> 5); lane slot s = lane & 31 of row t takes the 16 bytes of values 8 (s ^ (t & 7)) .. + 7,
+// and t & 7 = 2 w + (lane >> 5) does not depend on it, so the lane's byte column `col` is fixed. The rows' byte
+// offsets come from `rowtab`, laid out so that a lane's 16 are contiguous: rowtab[16 (t & 7) + (t >> 3)].
+//
+// The loads are issued from inline assembly so that the compiler, which cannot tell the two LDS buffers apart,
+// does not wait for them before the next LDS read of the other buffer; the K loop waits for them itself
+// (s_waitcnt vmcnt(0) and a barrier) before the buffer is read.
+constexpr int kStageIters = kTileBytes / (4 * 1024);  // 16
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+
+__device__ __forceinline__ void stage_async(uint32_t buf, const uint8_t* src, const uint32_t* rowtab, uint32_t col,
+                                            int wv, int half) {
+    const uint4* tab = reinterpret_cast<const uint4*>(rowtab + 16 * (2 * wv + half));
+    uint32_t off[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 v = tab[i];
+        off[4 * i] = v.x;
+        off[4 * i + 1] = v.y;
+        off[4 * i + 2] = v.z;
+        off[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int it = 0; it < kStageIters; it++) {
+        // M0 (the LDS destination) is a register the compiler reserves: saved and restored around the load
+        uint32_t saved;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+            : "=&s"(saved)
+            : "s"(buf + (4 * it + wv) * 1024), "v"(off[it] + col), "s"(src)
+            : "memory");
+    }
+}
+
+// A wavefront-uniform pointer in scalar registers (the value of lane 0).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Waits for every outstanding load, the inline-assembly ones included; the compiler sees this wait, so it does not
+// add waits of its own for loads issued before it.
+__device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
+
+// The K loop for NT token tiles. Block kc + 1's row states and LDS tile are requested at the top of iteration kc;
+// the last iteration requests the row states of its own block again (keeping the loop free of branches around the
+// register loads) and no tile.
+template <int TYPE, int NT, typename RowPtr>
+__device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[4][8], int nblocks,
+                                          const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr, int lr, int q) {
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
+    const uint32_t lds0 = lds_address(bufs[0]), lds1 = lds_address(bufs[1]);
+    const BAddr ba = b_addr(lr, q);
+    RowState<TYPE> rs[4], nx[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) rs[r].fetch(row_ptr(r, lr), q);
+    stage_async(lds0, src, rowtab, col, wv, half);
+    bf16x8 a0[4], a1[4], b[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) a0[r] = rs[r].template frag<0>(q);
+    for (int kc = 0; kc < nblocks; kc++) {
+        wait_stage();     // this chunk's LDS tile has landed
+        __syncthreads();  // ... for every wavefront, and the other buffer is free
+        const int kn = kc + 1 < nblocks ? kc + 1 : kc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
+        if (kc + 1 < nblocks) stage_async((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
+                                          rowtab, col, wv, half);
+        const uint8_t* buf = bufs[kc & 1];
+        read_b<NT, 0>(buf, ba, b);
+        gemm_step<TYPE, NT, 0>(buf, ba, rs, nx, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 1>(buf, ba, rs, nx, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 2>(buf, ba, rs, nx, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 3>(buf, ba, rs, nx, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 4>(buf, ba, rs, nx, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 5>(buf, ba, rs, nx, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 6>(buf, ba, rs, nx, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 7>(buf, ba, rs, nx, acc, a1, b, a0, q);
+#pragma unroll
+        for (int r = 0; r < 4; r++) rs[r] = nx[r];
+    }
+    wait_stage();
+}
+
 // ---------------------------------------------------------------------------------------------------------------
-// The GEMM core: a workgroup of 4 wavefronts, each owning 4 row tiles of 16 (rows given by row_ptr(r, lr)) and
-// the tile's (up to) 128 tokens as 8 token tiles. For each K chunk of 256 (one block per row) the activations are
-// staged in LDS, every wavefront fetches its rows' blocks, and each of the 8 32-value steps decodes 4 A-fragments
-// and runs up to 32 MFMAs.
+// The GEMM core: a workgroup of 4 wavefronts, each owning 4 row tiles of 16 (rows given by row_ptr(r, lr)) and the
+// tile's (up to) 128 tokens as 8 token tiles (4 when the tile has at most 64 tokens). Per K chunk of 256 values (one
+// block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes 4 A-fragments
+// and runs 4 x NT MFMAs. src_row(t) is token t's row in src ([*, ld] bf16); rows past count load token 0's (their
+// results are never stored).
 template <int TYPE, typename RowPtr, typename SrcRow>
-__device__ __forceinline__ void gemm_tile(uint16_t* lds, floatx4 (&acc)[4][8], int nblocks, int count,
-                                          const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
+__device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[4][8], int nblocks,
+                                          int count, const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
                                           RowPtr row_ptr) {
-    __shared__ int rows[kTileTokens];
+    __shared__ __attribute__((aligned(16))) uint32_t rowtab[kTileTokens];
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
-    const int ngroups = (count + 63) >> 6;
-    for (int t = threadIdx.x; t < count; t += blockDim.x) rows[t] = static_cast<int>(src_row(t));
+    for (int t = threadIdx.x; t < kTileTokens; t += blockDim.x)
+        rowtab[16 * (t & 7) + (t >> 3)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
         for (int n = 0; n < 8; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = 0; kc < nblocks; kc++) {
-        __syncthreads();
-        stage_tile(lds, src, ld, kc * kBK, count, rows);
-        RowState<TYPE> rs[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) rs[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kc) * BlockInfo<TYPE>::bytes, q);
-        __syncthreads();
-        gemm_step<TYPE, 0>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 1>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 2>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 3>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 4>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 5>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 6>(lds, rs, acc, ngroups, lr, q);
-        gemm_step<TYPE, 7>(lds, rs, acc, ngroups, lr, q);
-    }
+    __syncthreads();
+    const uint8_t* s8 = uniform_ptr(reinterpret_cast<const uint8_t*>(src));
+    if (count > 64)
+        gemm_loop<TYPE, 8>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+    else
+        gemm_loop<TYPE, 4>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
 }
 
-// gate_up: blockIdx.x = 128-row slab of the intermediate dim; wavefront w: gate rows j0 + 16r + lr (r = 0, 1)
-// and the matching up rows inter + j0 + ... (r = 2, 3), j0 = 128 bx + 32 w. Epilogue h = silu(g) * u -> bf16.
+// Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its own L2. slab_tile maps the linear
+// id to (row slab, tile) so that the nslab workgroups of one tile run back to back on one XCD and share its L2 copy of
+// the tile's activations: XCD x takes tiles x, x + 8, ..., each as nslab consecutive workgroups. The grid is
+// nslab * tiles8 workgroups, tiles8 = the tile bound rounded up to a multiple of 8.
+constexpr int kXcds = 8;
+__device__ __forceinline__ void slab_tile(int nslab, int& slab, int& tile) {
+    const int b = static_cast<int>(blockIdx.x), x = b % kXcds, i = b / kXcds;
+    slab = i % nslab;
+    tile = (i / nslab) * kXcds + x;
+}
+
+// gate_up: slab = 128-row slab of the intermediate dim; wavefront w: gate rows j0 + 16r + lr (r = 0, 1)
+// and the matching up rows inter + j0 + ... (r = 2, 3), j0 = 128 slab + 32 w. Epilogue h = silu(g) * u -> bf16.
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[kTileTokens * kLdsRow];
-    if (static_cast<int>(blockIdx.y) >= a.n_tiles[0]) return;
-    const int4 tile = a.tiles[blockIdx.y];
+    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
+    int slab, ti;
+    slab_tile(a.nslab_gate_up, slab, ti);
+    if (ti >= a.n_tiles[0]) return;
+    const int4 tile = a.tiles[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
-    const int j0 = blockIdx.x * 128 + 32 * (threadIdx.x >> 6);
-    if (static_cast<int>(blockIdx.x) * 128 >= inter) return;
+    const int j0 = slab * 128 + 32 * (threadIdx.x >> 6);
+    if (slab * 128 >= inter) return;
     const uint8_t* W = sh ? a.sh_gate_up : a.gate_up + static_cast<int64_t>(tile.x) * a.gate_up_stride;
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
@@ -378,7 +495,7 @@ __global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
         return W + static_cast<int64_t>((r < 2 ? 0 : inter) + j) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
-    gemm_tile<TYPE>(lds, acc, nb, count, a.xb, a.H, src_row, row_ptr);
+    gemm_tile<TYPE>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     uint16_t* out = sh ? a.h_sh16 : a.h16;
 #pragma unroll
@@ -397,15 +514,17 @@ __global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
     }
 }
 
-// down: blockIdx.x = 256-row slab of the hidden dim; wavefront w: rows r0 + 64 w + 16 r + lr. o fp32 by position.
+// down: slab = 256-row slab of the hidden dim; wavefront w: rows r0 + 64 w + 16 r + lr. o fp32 by position.
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_gemm_down(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[kTileTokens * kLdsRow];
-    if (static_cast<int>(blockIdx.y) >= a.n_tiles[0]) return;
-    const int4 tile = a.tiles[blockIdx.y];
+    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
+    int slab, ti;
+    slab_tile(a.H / 256, slab, ti);
+    if (ti >= a.n_tiles[0]) return;
+    const int4 tile = a.tiles[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
-    const int row0 = blockIdx.x * 256 + 64 * (threadIdx.x >> 6);
+    const int row0 = slab * 256 + 64 * (threadIdx.x >> 6);
     const uint8_t* W = sh ? a.sh_down : a.down + static_cast<int64_t>(tile.x) * a.down_stride;
     const int nb = inter / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
@@ -413,7 +532,7 @@ __global__ __launch_bounds__(256) void k_gemm_down(PrefillArgs a) {
     floatx4 acc[4][8];
     auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>(row0 + 16 * r + lr) * rs; };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
-    gemm_tile<TYPE>(lds, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
+    gemm_tile<TYPE>(bufs, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     float* out = sh ? a.o_sh : a.o;
 #pragma unroll
@@ -473,15 +592,16 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     a.sh_inter = shared ? L.shared_inter : 0;
     a.E = L.n_experts;
     a.k = L.top_k;
-    const int tiles = max_tiles(L, T);
+    const int tiles8 = (max_tiles(L, T) + kXcds - 1) / kXcds * kXcds;
     const int inter_max = shared && L.shared_inter > L.inter ? L.shared_inter : L.inter;
-    const dim3 g1(static_cast<unsigned>((inter_max + 127) / 128), static_cast<unsigned>(tiles));
+    a.nslab_gate_up = (inter_max + 127) / 128;
+    const dim3 g1(static_cast<unsigned>(a.nslab_gate_up * tiles8));
     // the routed and shared experts share one launch, so their types must agree (checked by prefill_eligible)
     if (L.gate_up_type == WL_TYPE_Q4_K)
         k_gemm_gate_up<WL_TYPE_Q4_K><<<g1, 256, 0, s>>>(a);
     else
         k_gemm_gate_up<WL_TYPE_Q6_K><<<g1, 256, 0, s>>>(a);
-    const dim3 g2(static_cast<unsigned>(L.hidden / 256), static_cast<unsigned>(tiles));
+    const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, 256, 0, s>>>(a);
     else
@@ -497,6 +617,9 @@ bool prefill_eligible(const WlMoeLayer& L, int64_t T) {
     if (L.shared_gate_up && (L.shared_gate_up_type != L.gate_up_type || L.shared_down_type != L.down_type ||
                              L.shared_inter % 128 != 0))
         return false;
+    // the LDS staging addresses activation rows by 32-bit byte offsets
+    const int64_t inter_max = L.shared_gate_up && L.shared_inter > L.inter ? L.shared_inter : L.inter;
+    if (T * L.hidden * 2 >= (int64_t{1} << 31) || T * L.top_k * inter_max * 2 >= (int64_t{1} << 31)) return false;
     return true;
 }
 
