@@ -146,8 +146,9 @@ def unique_experts(torch, layers, xs, T):
     return [int(torch.unique(ids).numel()) for ids in counts]
 
 
-def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label):
-    """One step = T tokens through every layer; returns timings and byte counts."""
+def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label, graph=True):
+    """One step = T tokens through every layer; returns timings and byte counts. graph=False launches the layers
+    eagerly (for counter collection, which sees dispatches made outside graphs)."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1000 + T)
     L = len(layers)
@@ -160,20 +161,30 @@ def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label):
         for l, layer in enumerate(layers):  # warm the kernels once outside capture
             layer(xset[l], out=ys[l], workspace=ws)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=capture):
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=capture):
+                for l, layer in enumerate(layers):
+                    layer(xset[l], out=ys[l], workspace=ws)
+            graphs.append(g)
+    torch.cuda.synchronize()
+
+    def step(i):
+        if graph:
+            graphs[i % n_sets].replay()
+        else:
+            xset = xs[i % n_sets]
             for l, layer in enumerate(layers):
                 layer(xset[l], out=ys[l], workspace=ws)
-        graphs.append(g)
-    torch.cuda.synchronize()
+
     for i in range(warmup):
-        graphs[i % n_sets].replay()
+        step(i)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
     for i in range(steps):
-        graphs[i % n_sets].replay()
+        step(i)
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -216,6 +227,18 @@ def profile_stages(torch, hip, layers, xs, T, ws, reps=2):
     return {n: sum(v) / len(v) for n, v in per.items()}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` from the committed counter summary (rocprofv3 FETCH_SIZE and WRITE_SIZE
+    runs of this script, each scaled by the same counter's reading for a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_decode_b1_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_dispatch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def cpu_baseline(budget_s=12.0):
     """The CPU oracle (numpy dequantize of the touched experts + fp32 BLAS matmuls): decode of single tokens
     through one full-shape layer, until the time budget is spent."""
@@ -249,14 +272,28 @@ def main():
     ap.add_argument("--skip-b64", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the decode layers eagerly instead of replaying HIP graphs (for counter runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB five times (the reference kernel for "
+                         "scaling FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's MoE layer runs on a single MI355X (expert-parallel "
               "sharding across GPUs is designed, not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
-    from gguf import hip
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return
+    from gguf import hip
     hip.library()
 
     log(f"building {args.layers} layers in HBM")
@@ -265,7 +302,8 @@ def main():
     torch.cuda.synchronize()
     log(f"built in {time.time() - t:.1f}s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated")
 
-    d1 = run_decode(torch, hip, layers, 1, args.steps, args.warmup, args.sets, "decode b=1")
+    d1 = run_decode(torch, hip, layers, 1, args.steps, args.warmup, args.sets, "decode b=1",
+                    graph=not args.no_graph)
     stages = profile_stages(torch, hip, layers, d1["xs"], 1, d1["ws"])
     log("stage us (b=1): " + ", ".join(f"{k} {v:.2f}" for k, v in stages.items()))
     U1 = sum(d1["unique"]) / len(d1["unique"])
@@ -293,24 +331,24 @@ def main():
         "hbm_frac": round(d1["hbm_gbps"] / HBM_PEAK_GBPS, 4),
         "stages_us_b1": {k: round(v, 3) for k, v in stages.items()},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "algorithmic_bytes": int(dom_bytes)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(dominant), "algorithmic_bytes": int(dom_bytes)},
     }
     del d1
+    if not args.skip_prefill:
+        result["prefill"] = run_prefill(torch, hip, layers, 4096, steps=2)
     if not args.skip_b64:
-        zl = build_layers(torch, hip, args.layers, zipf=True, seed=3) if True else None
         del layers
         torch.cuda.empty_cache()
-        d64 = run_decode(torch, hip, zl, 64, max(10, args.steps // 10), max(2, args.warmup // 4), 4, "decode b=64")
+        zl = build_layers(torch, hip, args.layers, zipf=True, seed=3)
+        d64 = run_decode(torch, hip, zl, 64, max(10, args.steps // 10), max(2, args.warmup // 4), 4, "decode b=64",
+                         graph=not args.no_graph)
         result["decode_b64"] = {"us_per_token_layer": round(d64["us_per_token_layer"], 3),
                                 "us_per_layer": round(d64["us_per_layer"], 2),
                                 "hbm_gbps": round(d64["hbm_gbps"], 1),
                                 "mean_unique_experts": round(sum(d64["unique"]) / len(d64["unique"]), 1),
                                 "routing": "Zipf(1.1) router bias"}
-        layers = zl
         del d64
-    if not args.skip_prefill:
-        result["prefill"] = run_prefill(torch, hip, layers, 4096, steps=2)
     if not args.skip_cpu:
         log("timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline()
@@ -337,7 +375,8 @@ def run_prefill(torch, hip, layers, T, steps):
     log(f"prefill T={T}: {ms:.1f} ms per chunk of {len(layers)} layers, {T / ms * 1e3:.0f} tok/s")
     return {"tokens": T, "ms_per_chunk": round(ms, 2), "tok_per_s": round(T / ms * 1e3, 1),
             "tflops": round(flops / ms / 1e9, 2), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
-            "path": "fp32 GEMV kernels (no MFMA yet)"}
+            "path": layers[0].plan(T) + ": tiled fp32 router, bf16 MFMA grouped expert GEMMs (in-register "
+                    "Q4_K/Q6_K dequant), fp32 combine"}
 
 
 if __name__ == "__main__":

@@ -108,15 +108,15 @@ int wl_moe_check(const WlMoeLayer* layer);
 /* Bytes of device workspace wl_moe_layer needs for `tokens` tokens (0 on an invalid layer). */
 size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
 
-/* Zeroes the synchronization words at the start of a workspace (the fused decode kernel's grid-barrier flags,
- * about 64 KiB) with a fill kernel on `stream`. Call once after allocating a workspace, before its first
+/* Zeroes the synchronization words at the start of a workspace (the fused decode kernel's per-workgroup epoch
+ * counters and epoch-tagged exchange slots) with a fill kernel on `stream`. Call once after allocating a workspace, before its first
  * wl_moe_layer; calls keep these words consistent afterwards. Calls that share one workspace must be ordered (one
  * stream): concurrent ones race. */
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Which path wl_moe_layer takes for `tokens` tokens: 1 = one fused persistent kernel (batch-1 decode at
- * Qwen3.6-like shapes), 0 = the multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an
- * invalid layer. */
+ * Qwen3.6-like shapes), 2 = bf16 MFMA grouped expert GEMMs (prefill: tokens * top_k >= 16 * n_experts), 0 = the
+ * fp32 multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an invalid layer. */
 int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens);
 
 /* Router: logits = x W_r^T (+ bias) in a fixed floating-point order: hidden is cut into segments of 64

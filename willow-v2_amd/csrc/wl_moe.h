@@ -73,7 +73,7 @@ struct PrefillArgs {
 };
 
 struct Workspace {
-    uint32_t* sync;     // [kSyncWords] grid-barrier words of the fused kernel (zeroed once, left zeroed)
+    uint32_t* sync;     // [kSyncWords] the fused kernel's epoch counters and tagged exchange slots (zeroed once)
     float* logits;      // [T, E + 1]
     float* sg;          // [T]      sigmoid(shared gate)
     int32_t* ids;       // [T, k]

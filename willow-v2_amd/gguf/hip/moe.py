@@ -126,7 +126,7 @@ class MoELayer:
 
 
 def new_workspace(nbytes: int, device) -> torch.Tensor:
-    """A device workspace with its grid-barrier words zeroed (wl_moe_workspace_init), ready for any layer."""
+    """A device workspace with its synchronization words zeroed (wl_moe_workspace_init), ready for any layer."""
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
     check(library().wl_moe_workspace_init(ws.data_ptr(), ws.numel(), _stream(ws.device)))
     return ws
