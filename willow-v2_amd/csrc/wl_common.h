@@ -55,10 +55,16 @@ __device__ __forceinline__ float ubyte(uint32_t w, int n) { return static_cast<f
 // 16 bytes from a 2-byte-aligned address, read as 5 aligned dwords and realigned with v_alignbyte. Every caller
 // stays inside its 210-byte Q6_K block: the extra bytes read lie at most 2 before and 4 after the 16 wanted ones,
 // and the ranges used (ql: block offsets 0..131, qh: 126..195) are inside the block.
+// The aligned address is formed by subtracting from the byte pointer (not rebuilt from an integer), so the compiler
+// keeps the pointer's global address space and emits global loads, not flat ones.
+__device__ __forceinline__ const uint32_t* align_down4(const uint8_t* p, uint32_t& sh) {
+    sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+    return reinterpret_cast<const uint32_t*>(p - sh);
+}
+
 __device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
-    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    uint32_t sh;
+    const uint32_t* q = align_down4(p, sh);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
     uint4 r;
     r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
@@ -141,6 +147,72 @@ __device__ __forceinline__ void decode(const uint8_t* __restrict__ blk, int c, L
     else
         decode_q6k(blk, c, o);
 }
+
+// decode() split in two: fetch() only issues the lane's loads (raw words kept as loaded), unpack() does the
+// arithmetic later, so code placed between them does not wait for the loads. unpack(fetch(b)) == decode(b).
+template <int TYPE>
+struct RawLane;
+template <>
+struct RawLane<WL_TYPE_Q4_K> {
+    uint4 hd, qv;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ blk, int c) {
+        hd = *reinterpret_cast<const uint4*>(blk);
+        qv = *reinterpret_cast<const uint4*>(blk + 16 + 16 * c);
+    }
+    __device__ __forceinline__ void unpack(int c, Lane32& o) const {
+        const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
+        const int j0 = 2 * (c >> 1);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(j0, hd.y, hd.z, hd.w, sc0, m0);
+        q4k_scale_min(j0 + 1, hd.y, hd.z, hd.w, sc1, m1);
+        o.a_lo = d * static_cast<float>(sc0);
+        o.b_lo = -(dmin * static_cast<float>(m0));
+        o.a_hi = d * static_cast<float>(sc1);
+        o.b_hi = -(dmin * static_cast<float>(m1));
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o.lo[i] = q[i] & 0x0F0F0F0Fu;
+            o.hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+        }
+    }
+};
+template <>
+struct RawLane<WL_TYPE_Q6_K> {
+    uint32_t l[5], h[5];  // the aligned dwords around the lane's 16 ql and 16 qh bytes
+    uint32_t lsh, hsh;    // their misalignment (0 or 2)
+    uint32_t d16, s_lo, s_hi;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ blk, int c) {
+        const int hh = c >> 2, t0 = (c >> 1) & 1, half = c & 1;
+        const uint32_t* ql = align_down4(blk + 16 * c, lsh);
+        const uint32_t* qh = align_down4(blk + 128 + 32 * hh + 16 * half, hsh);
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            l[i] = ql[i];
+            h[i] = qh[i];
+        }
+        d16 = *reinterpret_cast<const uint16_t*>(blk + 208);
+        const int lo_idx = 8 * hh + 2 * t0 + half;
+        s_lo = blk[192 + lo_idx];
+        s_hi = blk[192 + lo_idx + 4];
+    }
+    __device__ __forceinline__ void unpack(int c, Lane32& o) const {
+        const int t0 = (c >> 1) & 1;
+        const float d = half_to_float(d16);
+        o.a_lo = d * static_cast<float>(static_cast<int8_t>(s_lo));
+        o.a_hi = d * static_cast<float>(static_cast<int8_t>(s_hi));
+        o.b_lo = -32.0f * o.a_lo;
+        o.b_hi = -32.0f * o.a_hi;
+        const uint32_t sh = 2 * t0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t l4 = __builtin_amdgcn_alignbyte(l[i + 1], l[i], lsh);
+            const uint32_t h2 = __builtin_amdgcn_alignbyte(h[i + 1], h[i], hsh);
+            o.lo[i] = (l4 & 0x0F0F0F0Fu) | (((h2 >> sh) & 0x03030303u) << 4);
+            o.hi[i] = ((l4 >> 4) & 0x0F0F0F0Fu) | (((h2 >> (sh + 4)) & 0x03030303u) << 4);
+        }
+    }
+};
 
 // The dequantized value of byte n of a run word: bit-exact with the CPU dequantizers (every product is exact,
 // so the fused multiply-add rounds once, as the CPU's separate multiply and subtract do).

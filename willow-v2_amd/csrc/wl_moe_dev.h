@@ -15,11 +15,11 @@ __device__ __forceinline__ float router_row(const float* __restrict__ x, const f
                                             int H, int lane) {
     const int slot = lane & 31, src_base = lane & 32;
     const int nseg = H / kRouterSeg;
-    float p[kRouterMaxJ];
-#pragma unroll
-    for (int j = 0; j < kRouterMaxJ; j++) p[j] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRouterMaxJ; j++) {
+    float total = 0.0f;
+    // one round per 32 segments (a single round up to H = 2048), kept as a loop so the body is emitted once
+#pragma unroll 1
+    for (int j = 0; 32 * j < nseg; j++) {
+        float p = 0.0f;
         const int s = slot + 32 * j;
         if (valid && s < nseg) {
             const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
@@ -27,26 +27,20 @@ __device__ __forceinline__ float router_row(const float* __restrict__ x, const f
 #pragma unroll
             for (int i = 0; i < kRouterSeg / 4; i++) {
                 const float4 wv = wp[i], xv = xp[i];
-                p[j] = __builtin_fmaf(xv.x, wv.x, p[j]);
-                p[j] = __builtin_fmaf(xv.y, wv.y, p[j]);
-                p[j] = __builtin_fmaf(xv.z, wv.z, p[j]);
-                p[j] = __builtin_fmaf(xv.w, wv.w, p[j]);
+                p = __builtin_fmaf(xv.x, wv.x, p);
+                p = __builtin_fmaf(xv.y, wv.y, p);
+                p = __builtin_fmaf(xv.z, wv.z, p);
+                p = __builtin_fmaf(xv.w, wv.w, p);
             }
         }
-    }
-    // gather the half's 32 partials of each j first (independent shuffles), then add them in segment order
-    float total = 0.0f;
+        // gather the half's 32 partials first (independent shuffles), then add them in segment order
+        float parts[32];
 #pragma unroll
-    for (int j = 0; j < kRouterMaxJ; j++) {
-        if (32 * j < nseg) {
-            float parts[32];
+        for (int sl = 0; sl < 32; sl++) parts[sl] = __shfl(p, src_base + sl);
 #pragma unroll
-            for (int sl = 0; sl < 32; sl++) parts[sl] = __shfl(p[j], src_base + sl);
-#pragma unroll
-            for (int sl = 0; sl < 32; sl++) {
-                const int s = sl + 32 * j;
-                if (s < nseg) total = s == 0 ? parts[sl] : __fadd_rn(total, parts[sl]);
-            }
+        for (int sl = 0; sl < 32; sl++) {
+            const int sg = sl + 32 * j;
+            if (sg < nseg) total = sg == 0 ? parts[sl] : __fadd_rn(total, parts[sl]);
         }
     }
     return total;
@@ -64,9 +58,18 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 // added in pick order, when renorm), and id_rank = its position among the k ids in ascending order.
 // The k-th largest key is found by a bitwise radix select over ballots (32 steps, no cross-lane latency chain);
 // the k picks are then compacted and ranked through `scratch` (64 words of LDS owned by this wavefront).
+// scratch must point to LDS. It is not volatile (volatile accesses keep the generic address space and become flat
+// instructions, each waiting on two counters); lane_sync orders the writes of one lane before the reads of another:
+// a wavefront's LDS instructions complete in issue order, so only the compiler has to be kept from moving them.
+__device__ __forceinline__ void lane_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int EJ>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, int k, bool renorm,
-                                          volatile uint32_t* scratch, int lane, int& out_id, float& out_w,
+                                          uint32_t* scratch, int lane, int& out_id, float& out_w,
                                           int& out_id_rank) {
     float v[EJ];
     uint32_t key[EJ];
@@ -89,13 +92,21 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, i
         if (valid[j]) s += expf(v[j] - m);
     s = group_sum<64>(s);
 
+    // K = the largest key with at least k keys >= K. The EJ ballots of a step are independent (counted after all
+    // are taken); once exactly k keys are >= a candidate the selected set is decided and the search stops.
     uint32_t K = 0;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = K | (1u << bit);
+        uint64_t m[EJ];
+#pragma unroll
+        for (int j = 0; j < EJ; j++) m[j] = __ballot(valid[j] && key[j] >= cand);
         int cnt = 0;
 #pragma unroll
-        for (int j = 0; j < EJ; j++) cnt += __popcll(__ballot(valid[j] && key[j] >= cand));
-        if (cnt >= k) K = cand;
+        for (int j = 0; j < EJ; j++) cnt += __popcll(m[j]);
+        if (cnt >= k) {
+            K = cand;
+            if (cnt == k) break;
+        }
     }
     int n_gt = 0;
 #pragma unroll
@@ -118,7 +129,7 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, i
         ties_before += __popcll(eq);
         picked_before += __popcll(sm);
     }
-    __builtin_amdgcn_wave_barrier();
+    lane_sync();
     // lane r < k ranks compacted pick r among the k (descending value, ties to the lower id) and by id, and puts
     // it at its descending position in the second half of scratch (id in bits 0..15, id rank in 16..31)
     if (lane < k) {
@@ -134,7 +145,7 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, i
         scratch[32 + 2 * desc] = mine.x;
         scratch[32 + 2 * desc + 1] = mine.y | (static_cast<uint32_t>(id_rank) << 16);
     }
-    __builtin_amdgcn_wave_barrier();
+    lane_sync();
     int my_id = 0;
     float my_v = -INFINITY;
     out_id_rank = 0;

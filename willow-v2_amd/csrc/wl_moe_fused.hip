@@ -2,20 +2,26 @@
 // down / combine as six launches), which is what bounds batch-1 decode: every launch costs microseconds while a
 // layer moves only ~20 MB.
 //
-// A persistent grid of G workgroups (one per CU, 8 wavefronts each) in two roles:
-//   gate_up workgroups  A: the router's logits (2 rows per wavefront task) and the shared expert's gate_up rows,
-//                          neither of which depends on the routing;
-//                       then: the routing (wave_topk over the logits, once all have arrived), then the picked
-//                          experts' gate_up rows into h, several rows per wavefront, all fetched before any is
-//                          computed. Then they exit.
-//   down workgroups     fetch the shared expert's down rows, wait for the logits, route, fetch the picked
-//                          experts' down rows into registers, wait for h_shared (shared expert's SwiGLU output)
-//                          and dot it, wait for h, then write y = sum_e w_e (down_e h_e) + sg * shared_down h_sh,
-//                          experts in ascending id. R output rows per wavefront.
-// The arithmetic (router_row, wave_topk, the gate_up and down dot products, the combine order) is the multi-kernel
-// path's.
+// A persistent grid of G workgroups (one per CU, 8 wavefronts each), all in the same role:
+//   phase A   the router's logits (2 rows per wavefront task) and the shared expert's gate_up rows (h_shared),
+//             neither of which depends on the routing; each workgroup also loads the shared expert's down rows of
+//             the output rows it owns (8 per workgroup);
+//   routing   every workgroup gathers the logits and h_shared and runs the top-k itself (wavefront 0);
+//   phase B   every wavefront issues the loads of all its work at once: its gate_up tasks (a gate row and its up
+//             row of one picked expert) and its 8 rows of one picked expert's down matrix (workgroup chunks of
+//             64 rows), kept as raw words; while they are in flight the owners dot their shared down rows with
+//             h_shared; then the gate_up rows are decoded and dotted, and h (silu(g) * u) published;
+//   down      a workgroup gathers the h of its chunk's expert only (I values), dots its 64 rows and publishes the
+//             partial sums P[slot][row];
+//   combine   each owner gathers the k partials of its 8 rows and writes y = sum_e w_e P_e + sg * shared_down h_sh,
+//             experts in ascending id.
+// fused_eligible requires a grid large enough for one pass: at most one down chunk and one owner group per
+// workgroup and kGateUpTasks gate_up tasks per wavefront (Qwen3.6's shapes on 256 CUs use every workgroup).
+// Every CU streams its share of the routed experts' bytes (gate_up and down) from the moment the routing is known.
+// The arithmetic (router_row, wave_topk, the gate_up and down dot products, the combine order) is the
+// multi-kernel path's.
 //
-// No barriers: every value that crosses workgroups (logits, h_shared, h) is a 64-bit word (tag << 32 | bits)
+// No barriers: every value that crosses workgroups (logits, h_shared, h, P) is a 64-bit word (tag << 32 | bits)
 // written and read with relaxed device-scope atomics (single-copy atomic, bypassing the per-XCD L2s). The tag is
 // this call's epoch, so a consumer polls the data itself until every word it needs carries the current tag.
 // Each workgroup keeps its own epoch counter (one 128-byte line each, incremented as it exits), so all agree on
@@ -32,7 +38,9 @@ namespace wl {
 
 constexpr int kFusedThreads = 512;
 constexpr int kFusedWaves = kFusedThreads / 64;
-constexpr int kGateUpTasks = 4;  // gate_up rows a wavefront fetches before computing
+constexpr int kGateUpTasks = 2;  // gate_up tasks a wavefront has in flight at once (G = 256: all of them)
+constexpr int kChunkRows = 64;   // routed down rows per workgroup chunk (8 per wavefront)
+constexpr int kOwnRows = 8;      // output rows per owner group: shared down rows and the final sum
 constexpr uint32_t kSpinLimit = 1u << 20;
 
 struct FusedArgs {
@@ -49,7 +57,7 @@ struct FusedArgs {
     float* y;
     int32_t* ids_out;
     float* wts_out;
-    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I]
+    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I], P [k, H]
     int H, I, E, k, renorm, G;
 };
 
@@ -59,10 +67,10 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Copies the n tagged words at src into lds once every one carries `tag` (workgroup-cooperative); false if
-// kSpinLimit polls pass first. n <= 32 * blockDim.x.
-__device__ __forceinline__ bool gather_tagged(const uint32_t* src, int n, uint32_t tag, float* lds) {
-    const uint64_t* p = reinterpret_cast<const uint64_t*>(src);
+// Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset) into *dst(i) once
+// every one carries `tag` (workgroup-cooperative); false if kSpinLimit polls pass first. n <= 32 * blockDim.x.
+template <typename Src, typename Dst>
+__device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, Src src, Dst dst) {
     uint32_t pending = 0;
     for (int q = 0; q < 32 && static_cast<int>(threadIdx.x) + q * static_cast<int>(blockDim.x) < n; q++)
         pending |= 1u << q;
@@ -72,10 +80,10 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* src, int n, uint32
             const int q = __builtin_ctz(m);
             m &= m - 1;
             const int i = threadIdx.x + q * blockDim.x;
-            const uint64_t w = __hip_atomic_load(const_cast<uint64_t*>(p + i), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(i)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (static_cast<uint32_t>(w >> 32) == tag) {
-                lds[i] = __builtin_bit_cast(float, static_cast<uint32_t>(w));
+                *dst(i) = __builtin_bit_cast(float, static_cast<uint32_t>(w));
                 pending &= ~(1u << q);
             }
         }
@@ -87,173 +95,209 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* src, int n, uint32
 
 template <int GU, int DN, int EJ, int NBD>
 __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
-    constexpr int R = 8 / NBD, WIDTH = 8 * NBD;
-    __shared__ float lds_h[kFusedMaxK * kFusedMaxInter];
+    constexpr int WIDTH = 8 * NBD;  // lanes per down row (8 per block)
+    constexpr int R = 64 / WIDTH;   // down rows per wavefront pass
+    __shared__ float lds_h[kFusedMaxInter];
     __shared__ float lds_hsh[kFusedMaxInter];
     __shared__ float lds_logits[kFusedMaxE + 1];
     __shared__ int lds_sel[kFusedMaxK];
     __shared__ float lds_wsel[kFusedMaxK];
+    __shared__ float lds_sh[kOwnRows];
+    __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ uint32_t tk_scratch[64];
-    __shared__ uint32_t lds_epoch;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int G = a.G;
+    const int b = blockIdx.x, G = a.G;
     const int H = a.H, I = a.I, E = a.E, k = a.k;
     const bool shared = a.sh_gate_up != nullptr;
     const bool sh_gate = shared && a.sh_gate != nullptr;
     const int n_logits = E + (sh_gate ? 1 : 0);
     const int gi = lane >> 3, c = lane & 7;
-    const int ND = H / R;                                    // down wavefronts
-    const int NDW = (ND + kFusedWaves - 1) / kFusedWaves;    // down workgroups: blocks [0, NDW)
-    const bool down_wg = static_cast<int>(blockIdx.x) < NDW;
-    uint32_t* epoch_word = a.sync + kFlagStride * blockIdx.x;
+    const int NW = G * kFusedWaves;
+    const int slot = wv * G + b;  // wavefront slot: consecutive slots on different CUs
+    constexpr int64_t dn_rs = static_cast<int64_t>(NBD) * BlockInfo<DN>::bytes;
+    // a lane's place in a down row: block kb, and its two 16-value runs of h
+    const int drow = lane / WIDTH, kb = (lane % WIDTH) >> 3;
+    const int lo = kb * kQK + BlockInfo<DN>::lo_start(c), hi = lo + BlockInfo<DN>::hi_offset;
+    uint32_t* epoch_word = a.sync + kFlagStride * b;
 
-    if (threadIdx.x == 0) lds_epoch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const uint32_t tag = lds_epoch + 1u;
+    // every thread reads the epoch itself: no barrier, and the load overlaps the first weight loads
+    const uint32_t tag = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     bool ok = true;
 
-    // The routing from the logits, by wavefront 0; every wavefront reads it from LDS afterwards.
-    auto route = [&]() {
-        ok = gather_tagged(a.sync + kTagLogits, n_logits, tag, lds_logits) && ok;
-        if (wv == 0) {
-            int my_id, my_rank;
-            float my_w;
-            wave_topk<EJ>(lds_logits, E, k, a.renorm != 0, tk_scratch, lane, my_id, my_w, my_rank);
-            if (lane < k) {
-                lds_sel[my_rank] = my_id;
-                lds_wsel[my_rank] = my_w;
-                if (blockIdx.x == 0) {
-                    if (a.ids_out) a.ids_out[lane] = my_id;
-                    if (a.wts_out) a.wts_out[lane] = my_w;
-                }
-            }
+    // x, for the gate_up dot products: a lane's two 16-value runs of its block gi
+    const int nb = H / kQK;  // <= 8: one gate/up block per lane group
+    const bool gu_lane = gi < nb;
+    const int lo_gu = gi * kQK + BlockInfo<GU>::lo_start(c), hi_gu = lo_gu + BlockInfo<GU>::hi_offset;
+    const int64_t gu_rs = static_cast<int64_t>(nb) * BlockInfo<GU>::bytes;
+    float4 xl[4], xh[4];  // loaded now; their sums are taken where they are used, so nothing waits for x here
+    if (gu_lane) {
+        load_run(a.x + lo_gu, xl);
+        load_run(a.x + hi_gu, xh);
+    }
+    auto gate_up_dots = [&](const Lane32& lg, const Lane32& lu, float& g, float& u) {
+        float ag = 0.0f, au = 0.0f;
+        if (gu_lane) {
+            const float sxl = sum16(xl), sxh = sum16(xh);
+            ag = lane_dot_s(lg, xl, xh, sxl, sxh);
+            au = lane_dot_s(lu, xl, xh, sxl, sxh);
         }
-        __syncthreads();
+        g = group_sum<64>(ag);
+        u = group_sum<64>(au);
     };
 
-    if (down_wg) {
-        const int d = blockIdx.x * kFusedWaves + wv;
-        const bool dwave = d < ND;
-        const int row = d * R + gi / NBD, kb = gi % NBD;
-        constexpr int64_t dn_rs = static_cast<int64_t>(NBD) * BlockInfo<DN>::bytes;
-        const int lo = kb * kQK + BlockInfo<DN>::lo_start(c), hi = lo + BlockInfo<DN>::hi_offset;
-        Lane32 shl;
-        if (shared && dwave) decode<DN>(a.sh_down + row * dn_rs + kb * BlockInfo<DN>::bytes, c, shl);
-        route();
-        Lane32 pre[kFusedMaxK];
-        float wsel[kFusedMaxK];
-#pragma unroll
-        for (int s = 0; s < kFusedMaxK; s++) {
-            wsel[s] = lds_wsel[s];
-            if (s < k && dwave)
-                decode<DN>(a.down + static_cast<int64_t>(lds_sel[s]) * a.down_stride + row * dn_rs +
-                               kb * BlockInfo<DN>::bytes, c, pre[s]);
-        }
-        float sh_dot = 0.0f, sgv = 1.0f;
-        if (shared) {
-            ok = gather_tagged(a.sync + kTagHsh, I, tag, lds_hsh) && ok;
-            if (sh_gate) sgv = sigmoid(lds_logits[E]);
-            if (dwave) {
-                float4 hl[4], hh[4];
-                load_run(lds_hsh + lo, hl);
-                load_run(lds_hsh + hi, hh);
-                sh_dot = group_sum<WIDTH>(lane_dot(shl, hl, hh));
-            }
-        }
-        ok = gather_tagged(a.sync + kTagH, k * I, tag, lds_h) && ok;
-        if (dwave) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int s = 0; s < kFusedMaxK; s++) {
-                if (s < k) {
-                    float4 hl[4], hh[4];
-                    load_run(lds_h + s * I + lo, hl);
-                    load_run(lds_h + s * I + hi, hh);
-                    const float dv = group_sum<WIDTH>(lane_dot(pre[s], hl, hh));
-                    acc = s == 0 ? wsel[s] * dv : acc + wsel[s] * dv;
-                }
-            }
-            if (shared) acc = acc + sgv * sh_dot;
-            if ((lane & (WIDTH - 1)) == 0) a.y[row] = ok ? acc : __builtin_nanf("");
-        }
-    } else {
-        const int NG = G - NDW;
-        const int gslot = wv * NG + (static_cast<int>(blockIdx.x) - NDW);  // consecutive slots on different CUs
-        const int NWg = NG * kFusedWaves;
-        const int nb = H / kQK;  // <= 8: one gate/up block per lane group
-        const bool gu_lane = gi < nb;
-        const int lo_gu = gi * kQK + BlockInfo<GU>::lo_start(c), hi_gu = lo_gu + BlockInfo<GU>::hi_offset;
-        const int64_t gu_rs = static_cast<int64_t>(nb) * BlockInfo<GU>::bytes;
-        float4 xl[4], xh[4];
-        float sxl = 0.0f, sxh = 0.0f;
-        if (gu_lane) {
-            load_run(a.x + lo_gu, xl);
-            load_run(a.x + hi_gu, xh);
-            sxl = sum16(xl);
-            sxh = sum16(xh);
-        }
-        auto gate_up_dots = [&](const Lane32& lg, const Lane32& lu, float& g, float& u) {
-            float ag = 0.0f, au = 0.0f;
+    // workgroup b < H / kOwnRows owns output rows kOwnRows b .. + kOwnRows - 1; wavefront w < 8 / R takes rows
+    // kOwnRows b + R w + drow of the shared down matrix (fetched now, used once h_shared is known)
+    const bool owner = b < H / kOwnRows;
+    const bool sh_wave = wv < kOwnRows / R;
+    RawLane<DN> shraw;
+    if (shared && sh_wave && owner)
+        shraw.fetch(a.sh_down + static_cast<int64_t>(kOwnRows * b + R * wv + drow) * dn_rs +
+                        kb * BlockInfo<DN>::bytes, c);
+
+    // phase A: router rows, shared gate_up rows
+    const int n_router = (n_logits + 1) / 2;
+    const int n_a = n_router + (shared ? I : 0);
+    for (int t = slot; t < n_a; t += NW) {
+        if (t < n_router) {
+            const int row = 2 * t + (lane >> 5);
+            const bool valid = row < n_logits;
+            const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
+            const float total = router_row(a.x, wr, valid, H, lane);
+            if ((lane & 31) == 0 && valid)
+                put_tagged(a.sync, kTagLogits + 2 * row, tag,
+                           (row < E && a.router_bias) ? __fadd_rn(total, a.router_bias[row]) : total);
+        } else {
+            const int j = t - n_router;
+            Lane32 lg, lu;
             if (gu_lane) {
-                ag = lane_dot_s(lg, xl, xh, sxl, sxh);
-                au = lane_dot_s(lu, xl, xh, sxl, sxh);
+                decode<GU>(a.sh_gate_up + j * gu_rs + gi * BlockInfo<GU>::bytes, c, lg);
+                decode<GU>(a.sh_gate_up + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c, lu);
             }
-            g = group_sum<64>(ag);
-            u = group_sum<64>(au);
-        };
-        // phase A: router rows, shared gate_up rows
-        const int n_router = (n_logits + 1) / 2;
-        const int n_a = n_router + (shared ? I : 0);
-        for (int t = gslot; t < n_a; t += NWg) {
-            if (t < n_router) {
-                const int row = 2 * t + (lane >> 5);
-                const bool valid = row < n_logits;
-                const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
-                const float total = router_row(a.x, wr, valid, H, lane);
-                if ((lane & 31) == 0 && valid)
-                    put_tagged(a.sync + kTagLogits, 2 * row, tag,
-                               (row < E && a.router_bias) ? __fadd_rn(total, a.router_bias[row]) : total);
-            } else {
-                const int j = t - n_router;
-                Lane32 lg, lu;
-                if (gu_lane) {
-                    decode<GU>(a.sh_gate_up + j * gu_rs + gi * BlockInfo<GU>::bytes, c, lg);
-                    decode<GU>(a.sh_gate_up + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c, lu);
-                }
-                float g, u;
-                gate_up_dots(lg, lu, g, u);
-                if (lane == 0) put_tagged(a.sync + kTagHsh, 2 * j, tag, silu(g) * u);
+            float g, u;
+            gate_up_dots(lg, lu, g, u);
+            if (lane == 0) put_tagged(a.sync, kTagHsh + 2 * j, tag, silu(g) * u);
+        }
+    }
+
+    // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
+    // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading.
+    __syncthreads();
+    ok = gather_tagged(
+             a.sync, n_logits + (shared ? I : 0), tag,
+             [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
+             [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
+         ok;
+    if (wv == 0) {
+        int my_id, my_rank;
+        float my_w;
+        wave_topk<EJ>(lds_logits, E, k, a.renorm != 0, tk_scratch, lane, my_id, my_w, my_rank);
+        if (lane < k) {
+            lds_sel[my_rank] = my_id;
+            lds_wsel[my_rank] = my_w;
+            if (b == 0) {
+                if (a.ids_out) a.ids_out[lane] = my_id;
+                if (a.wts_out) a.wts_out[lane] = my_w;
             }
         }
-        route();
-        int sel[kFusedMaxK];
+    }
+    __syncthreads();
+    int sel[kFusedMaxK];
 #pragma unroll
-        for (int s = 0; s < kFusedMaxK; s++) sel[s] = lds_sel[s];
-        for (int u0 = gslot; u0 < k * I; u0 += NWg * kGateUpTasks) {
-            Lane32 lg[kGateUpTasks], lu[kGateUpTasks];
+    for (int s = 0; s < kFusedMaxK; s++) sel[s] = lds_sel[s];
+    auto expert_of = [&](int s) {
+        int e = 0;
 #pragma unroll
-            for (int q = 0; q < kGateUpTasks; q++) {
-                const int u = u0 + q * NWg;
-                if (u < k * I && gu_lane) {
-                    const int s = u / I, j = u - s * I;
-                    int e = 0;
+        for (int r = 0; r < kFusedMaxK; r++)
+            if (r == s) e = sel[r];
+        return e;
+    };
+
+    // phase B: every load of this wavefront's gate_up tasks (at most kGateUpTasks, fused_grid_fits) and of its
+    // workgroup's down chunk (at most one), before any arithmetic
+    const int n_tasks = k * I;
+    RawLane<GU> graw[kGateUpTasks][2];
 #pragma unroll
-                    for (int r = 0; r < kFusedMaxK; r++)
-                        if (r == s) e = sel[r];
-                    const uint8_t* w = a.gate_up + static_cast<int64_t>(e) * a.gate_up_stride;
-                    decode<GU>(w + j * gu_rs + gi * BlockInfo<GU>::bytes, c, lg[q]);
-                    decode<GU>(w + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c, lu[q]);
-                }
+    for (int q = 0; q < kGateUpTasks; q++) {
+        const int u = slot + q * NW;
+        if (u < n_tasks && gu_lane) {
+            const int s = u / I, j = u - s * I;
+            const uint8_t* w = a.gate_up + static_cast<int64_t>(expert_of(s)) * a.gate_up_stride;
+            graw[q][0].fetch(w + j * gu_rs + gi * BlockInfo<GU>::bytes, c);
+            graw[q][1].fetch(w + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c);
+        }
+    }
+    const int chunks_per_expert = H / kChunkRows;
+    const bool has_chunk = b < k * chunks_per_expert;
+    const int cs = b / chunks_per_expert;  // the chunk's expert slot
+    auto chunk_row = [&](int pass) { return (b % chunks_per_expert) * kChunkRows + 8 * wv + R * pass + drow; };
+    RawLane<DN> draw[NBD];
+    if (has_chunk) {
+        const uint8_t* w = a.down + static_cast<int64_t>(expert_of(cs)) * a.down_stride;
+#pragma unroll
+        for (int p = 0; p < NBD; p++)
+            draw[p].fetch(w + static_cast<int64_t>(chunk_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
+    }
+
+    // the shared expert's down rows of this workgroup's owner group, while the loads above are in flight
+    float sgv = 1.0f;
+    if (sh_gate) sgv = sigmoid(lds_logits[E]);
+    if (shared && sh_wave && owner) {
+        Lane32 w;
+        shraw.unpack(c, w);
+        float4 hl[4], hh[4];
+        load_run(lds_hsh + lo, hl);
+        load_run(lds_hsh + hi, hh);
+        const float v = group_sum<WIDTH>(lane_dot(w, hl, hh));
+        if ((lane % WIDTH) == 0) lds_sh[R * wv + drow] = v;
+    }
+
+    // gate_up: decode, dot, publish h[s][j]
+#pragma unroll
+    for (int q = 0; q < kGateUpTasks; q++) {
+        const int u = slot + q * NW;
+        if (u < n_tasks) {
+            Lane32 lg, lu;
+            if (gu_lane) {
+                graw[q][0].unpack(c, lg);
+                graw[q][1].unpack(c, lu);
             }
+            float g, up;
+            gate_up_dots(lg, lu, g, up);
+            if (lane == 0) put_tagged(a.sync, kTagH + 2 * u, tag, silu(g) * up);  // u = s * I + j
+        }
+    }
+
+    // down: the h of the chunk's expert, its 64 row dots, the partials published
+    if (has_chunk) {
+        ok = gather_tagged(
+                 a.sync, I, tag, [&](int i) { return kTagH + 2 * (cs * I + i); }, [&](int i) { return &lds_h[i]; }) &&
+             ok;
 #pragma unroll
-            for (int q = 0; q < kGateUpTasks; q++) {
-                const int u = u0 + q * NWg;
-                if (u < k * I) {
-                    float g, up;
-                    gate_up_dots(lg[q], lu[q], g, up);
-                    if (lane == 0) put_tagged(a.sync + kTagH, 2 * u, tag, silu(g) * up);  // u = s * I + j
-                }
-            }
+        for (int p = 0; p < NBD; p++) {
+            Lane32 w;
+            draw[p].unpack(c, w);
+            float4 hl[4], hh[4];
+            load_run(lds_h + lo, hl);
+            load_run(lds_h + hi, hh);
+            const float v = group_sum<WIDTH>(lane_dot(w, hl, hh));
+            if ((lane % WIDTH) == 0) put_tagged(a.sync, kTagP + 2 * (cs * H + chunk_row(p)), tag, v);
+        }
+    }
+
+    // combine: the owner's rows y[j] = sum_s w_s P[s][j] (+ sg * shared), s in ascending expert id
+    if (owner) {
+        ok = gather_tagged(
+                 a.sync, k * kOwnRows, tag,
+                 [&](int i) { return kTagP + 2 * ((i / kOwnRows) * H + kOwnRows * b + i % kOwnRows); },
+                 [&](int i) { return &lds_p[i]; }) &&
+             ok;
+        if (threadIdx.x < kOwnRows) {
+            const int r = threadIdx.x;
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++)
+                acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
+            if (shared) acc = acc + sgv * lds_sh[r];
+            a.y[kOwnRows * b + r] = ok ? acc : __builtin_nanf("");
         }
     }
     __syncthreads();
@@ -315,11 +359,12 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T) {
     if (L.shared_gate_up && (L.shared_inter != L.inter || L.shared_gate_up_type != L.gate_up_type ||
                              L.shared_down_type != L.down_type))
         return false;
+    if (L.hidden % kChunkRows != 0 || L.hidden > kFusedMaxHidden) return false;
+    // one pass per workgroup: a down chunk and an owner group each at most, kGateUpTasks per wavefront at most
     const int G = fused_grid();
-    if (G < 2) return false;
-    const int down_waves = L.hidden / (8 / nbd);
-    const int down_wgs = (down_waves + kFusedWaves - 1) / kFusedWaves;
-    return down_wgs <= G / 2;  // leaves at least half the workgroups for the router and gate_up work
+    const int64_t chunks = static_cast<int64_t>(L.top_k) * (L.hidden / kChunkRows);
+    const int64_t tasks = static_cast<int64_t>(L.top_k) * L.inter;
+    return G >= 1 && chunks <= G && L.hidden / kOwnRows <= G && tasks <= static_cast<int64_t>(kGateUpTasks) * kFusedWaves * G;
 }
 
 int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,

@@ -41,9 +41,8 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // 8 bytes from a 2-byte-aligned address: 3 aligned dwords, realigned. Reads [p & ~3, (p & ~3) + 12), within
 // [p - 2, p + 12); all three loads are unconditional so that no branch splits the wavefront.
 __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
-    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    uint32_t sh;
+    const uint32_t* q = align_down4(p, sh);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
     return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
 }
@@ -231,9 +230,8 @@ __device__ __forceinline__ void fetch_q6k(const uint8_t* __restrict__ blk, int q
     for (int h = 0; h < 2; h++) s.qh[h] = load8_a2(blk + 128 + 32 * h + 8 * q);
     // scales: bytes 192..207 from the 4 dwords of their aligned start (bytes 190..205 or 192..207) and, for a block
     // 2 bytes into a dword, bytes 206..207 as a 16-bit load (the realignment takes only its low half)
-    const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 192);
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
-    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    uint32_t sh;
+    const uint32_t* p = align_down4(blk + 192, sh);
     const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3];
     const uint32_t w4 = *reinterpret_cast<const uint16_t*>(blk + 206);
     s.sc = make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
