@@ -67,42 +67,79 @@ __device__ __forceinline__ void lane_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The softmax statistics of one token's logits lt[0..E) (one wavefront, EJ logits per lane: lane + 64 j): the
+// logits with NaN as -inf, their max m and the sum s of exp(l - m) (per lane in j order, then across the wave).
 template <int EJ>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, int k, bool renorm,
-                                          uint32_t* scratch, int lane, int& out_id, float& out_w,
-                                          int& out_id_rank) {
-    float v[EJ];
-    uint32_t key[EJ];
-    bool valid[EJ];
-    float m = -INFINITY;
+__device__ __forceinline__ void softmax_stats(const float* __restrict__ lt, int E, int lane, float (&v)[EJ],
+                                              bool (&valid)[EJ], float& m, float& s) {
+    m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EJ; j++) {
         const int idx = lane + 64 * j;
         valid[j] = idx < E;
         const float lv = valid[j] ? lt[idx] : -INFINITY;
         v[j] = lv == lv ? lv : -INFINITY;
-        key[j] = order_key(v[j]);
         m = fmaxf(m, v[j]);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    float s = 0.0f;
+    s = 0.0f;
 #pragma unroll
     for (int j = 0; j < EJ; j++)
         if (valid[j]) s += expf(v[j] - m);
     s = group_sum<64>(s);
+}
+
+// softmax_stats' sum s for a known max m (bitwise the same: per lane in j order, then across the wave).
+template <int EJ>
+__device__ __forceinline__ float softmax_sum(const float* __restrict__ lt, int E, int lane, float m) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EJ; j++) {
+        const int idx = lane + 64 * j;
+        if (idx < E) {
+            const float lv = lt[idx];
+            s += expf((lv == lv ? lv : -INFINITY) - m);
+        }
+    }
+    return group_sum<64>(s);
+}
+
+// The routing weight of pick r = lane (< k; my_v its logit): exp(l - m) / s, divided by the sum of the k picks'
+// weights added in pick order when renorm. Call with the whole wavefront.
+__device__ __forceinline__ float pick_weight(float my_v, float m, float s, int k, bool renorm, int lane) {
+    const float p = lane < k ? expf(my_v - m) / s : 0.0f;
+    float wsum = 0.0f;
+    for (int r = 0; r < k; r++) {
+        const float pr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), r));
+        wsum = r == 0 ? pr : wsum + pr;
+    }
+    return renorm ? p / wsum : p;
+}
+
+template <int EJ>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, int k, bool renorm,
+                                          uint32_t* scratch, int lane, int& out_id, float& out_w,
+                                          int& out_id_rank) {
+    float v[EJ];
+    bool valid[EJ];
+    float m, s;
+    softmax_stats<EJ>(lt, E, lane, v, valid, m, s);
+    uint32_t key[EJ];
+#pragma unroll
+    for (int j = 0; j < EJ; j++) key[j] = order_key(v[j]);
 
     // K = the largest key with at least k keys >= K. The EJ ballots of a step are independent (counted after all
     // are taken); once exactly k keys are >= a candidate the selected set is decided and the search stops.
     uint32_t K = 0;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = K | (1u << bit);
-        uint64_t m[EJ];
+        uint64_t bal[EJ];
 #pragma unroll
-        for (int j = 0; j < EJ; j++) m[j] = __ballot(valid[j] && key[j] >= cand);
+        for (int j = 0; j < EJ; j++) bal[j] = __ballot(valid[j] && key[j] >= cand);
         int cnt = 0;
 #pragma unroll
-        for (int j = 0; j < EJ; j++) cnt += __popcll(m[j]);
+        for (int j = 0; j < EJ; j++) cnt += __popcll(bal[j]);
         if (cnt >= k) {
             K = cand;
             if (cnt == k) break;
@@ -155,14 +192,8 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, i
         my_id = static_cast<int>(r.y & 0xFFFFu);
         out_id_rank = static_cast<int>(r.y >> 16);
     }
-    const float p = lane < k ? expf(my_v - m) / s : 0.0f;
-    float wsum = 0.0f;
-    for (int r = 0; r < k; r++) {
-        const float pr = __shfl(p, r);
-        wsum = r == 0 ? pr : wsum + pr;
-    }
     out_id = my_id;
-    out_w = renorm ? p / wsum : p;
+    out_w = pick_weight(my_v, m, s, k, renorm, lane);
 }
 
 // One intermediate row j of a fused [gate | up] matrix (gate row j, up row inter + j) times one token x, one

@@ -3,23 +3,25 @@
 // layer moves only ~20 MB.
 //
 // A persistent grid of G workgroups (one per CU, 8 wavefronts each), all in the same role:
-//   phase A   the router's logits (2 rows per wavefront task) and the shared expert's gate_up rows (h_shared),
+//   phase A   the router's logits (a row per wavefront task) and the shared expert's gate_up rows (h_shared),
 //             neither of which depends on the routing; each workgroup also loads the shared expert's down rows of
 //             the output rows it owns (8 per workgroup);
-//   routing   every workgroup gathers the logits and h_shared and runs the top-k itself (wavefront 0);
-//   phase B   every wavefront issues the loads of all its work at once: its gate_up tasks (a gate row and its up
-//             row of one picked expert) and its 8 rows of one picked expert's down matrix (workgroup chunks of
-//             64 rows), kept as raw words; while they are in flight the owners dot their shared down rows with
-//             h_shared; then the gate_up rows are decoded and dotted, and h (silu(g) * u) published;
-//   down      a workgroup gathers the h of its chunk's expert only (I values), dots its 64 rows and publishes the
-//             partial sums P[slot][row];
+//   routing   every workgroup gathers the logits and h_shared and runs the top-k itself (candidate ranks
+//             counted by the workgroup, the weights by wavefront 0);
+//   phase B   every wavefront issues the loads of its gate_up tasks (a gate row and its up row of one picked
+//             expert) at once, kept as raw words; while they are in flight the owners dot their shared down rows
+//             with h_shared; then the gate_up rows are decoded and dotted, and h (silu(g) * u) published;
+//   down      every wavefront requests its 8 rows of one picked expert's down matrix (workgroup chunks of 64 rows),
+//             which arrive while h crosses workgroups; a workgroup gathers the h of its chunk's expert only
+//             (I values), dots its 64 rows and publishes the partial sums P[slot][row];
 //   combine   each owner gathers the k partials of its 8 rows and writes y = sum_e w_e P_e + sg * shared_down h_sh,
 //             experts in ascending id.
 // fused_eligible requires a grid large enough for one pass: at most one down chunk and one owner group per
 // workgroup and kGateUpTasks gate_up tasks per wavefront (Qwen3.6's shapes on 256 CUs use every workgroup).
-// Every CU streams its share of the routed experts' bytes (gate_up and down) from the moment the routing is known.
-// The arithmetic (router_row, wave_topk, the gate_up and down dot products, the combine order) is the
-// multi-kernel path's.
+// Every CU streams its share of the routed experts' bytes: gate_up rows as soon as the routing is known, down rows
+// as soon as its gate_up work is done.
+// The arithmetic (router_row, the top-k's picks and weights, the gate_up and down dot products, the combine
+// order) is the multi-kernel path's.
 //
 // No barriers: every value that crosses workgroups (logits, h_shared, h, P) is a 64-bit word (tag << 32 | bits)
 // written and read with relaxed device-scope atomics (single-copy atomic, bypassing the per-XCD L2s). The tag is
@@ -42,6 +44,8 @@ constexpr int kGateUpTasks = 2;  // gate_up tasks a wavefront has in flight at o
 constexpr int kChunkRows = 64;   // routed down rows per workgroup chunk (8 per wavefront)
 constexpr int kOwnRows = 8;      // output rows per owner group: shared down rows and the final sum
 constexpr uint32_t kSpinLimit = 1u << 20;
+static_assert(kFusedThreads >= kFusedMaxE && kFusedMaxE % 32 == 0 && kFusedMaxE / 32 >= kFusedMaxK,
+              "the top-k gives every logit a thread and needs at least k groups of 32");
 
 struct FusedArgs {
     const uint8_t* gate_up;
@@ -104,7 +108,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_wsel[kFusedMaxK];
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
-    __shared__ uint32_t tk_scratch[64];
+    __shared__ uint64_t lds_key[kFusedMaxE];
+    __shared__ uint64_t lds_cand[kFusedMaxE];
+    __shared__ uint64_t lds_gmax[kFusedMaxE / 32];
+    __shared__ int lds_wcount[kFusedWaves];
+    __shared__ int lds_pick[kFusedMaxK];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int b = blockIdx.x, G = a.G;
     const int H = a.H, I = a.I, E = a.E, k = a.k;
@@ -155,12 +163,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                         kb * BlockInfo<DN>::bytes, c);
 
     // phase A: router rows, shared gate_up rows
-    const int n_router = (n_logits + 1) / 2;
+    const int n_router = n_logits;  // one router row per wavefront task (lanes 0..31), more tasks in parallel
     const int n_a = n_router + (shared ? I : 0);
     for (int t = slot; t < n_a; t += NW) {
         if (t < n_router) {
-            const int row = 2 * t + (lane >> 5);
-            const bool valid = row < n_logits;
+            const int row = t;
+            const bool valid = lane < 32;
             const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
             const float total = router_row(a.x, wr, valid, H, lane);
             if ((lane & 31) == 0 && valid)
@@ -187,11 +195,63 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
              [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
              [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
          ok;
+    // top-k by rank among candidates. Key: the order key and the inverted id (larger first, ties to the lower
+    // id; 64 bits, all distinct). T0 = the smallest of the 8 half-wavefront maxima over keys 0..255: at least 8
+    // distinct keys are >= T0, so the top k (k <= 8) are among the candidates key >= T0 (typically 8 to 20, all
+    // 256 at worst); each candidate counts the candidates above it, and the k of rank < k place themselves.
+    // Wavefront 0 then computes the weights as wave_topk does.
+    {
+        const int i = threadIdx.x;
+        uint64_t key = 0;  // below every logit's
+        if (i < kFusedMaxE) {
+            if (i < E) {
+                const float v = lds_logits[i];
+                key = (static_cast<uint64_t>(order_key(v == v ? v : -INFINITY)) << 32) | (0xFFFFFFFFu - i);
+            }
+            lds_key[i] = key;
+        }
+        __syncthreads();
+        if (i < kFusedMaxE / 32) {  // 8 threads: the maximum of keys 32 i .. 32 i + 31
+            uint64_t mx = 0;
+            for (int u = 0; u < 32; u++) mx = lds_key[32 * i + u] > mx ? lds_key[32 * i + u] : mx;
+            lds_gmax[i] = mx;
+        }
+        __syncthreads();
+        uint64_t t0 = lds_gmax[0];
+#pragma unroll
+        for (int g = 1; g < kFusedMaxE / 32; g++) t0 = lds_gmax[g] < t0 ? lds_gmax[g] : t0;
+        const bool cand = i < E && key >= t0;
+        // compaction: the candidates' keys in index order
+        const uint64_t wm = __ballot(cand);
+        if (lane == 0) lds_wcount[wv] = __popcll(wm);
+        __syncthreads();
+        int base = 0, n_cand = 0;
+#pragma unroll
+        for (int w = 0; w < kFusedWaves; w++) {
+            base += w < wv ? lds_wcount[w] : 0;
+            n_cand += lds_wcount[w];
+        }
+        if (cand) lds_cand[base + __popcll(wm & __lanemask_lt())] = key;
+        __syncthreads();
+        if (cand) {
+            int above = 0;
+            for (int u = 0; u < n_cand; u++) above += lds_cand[u] > key ? 1 : 0;
+            if (above < k) lds_pick[above] = i;
+        }
+        __syncthreads();
+    }
     if (wv == 0) {
-        int my_id, my_rank;
-        float my_w;
-        wave_topk<EJ>(lds_logits, E, k, a.renorm != 0, tk_scratch, lane, my_id, my_w, my_rank);
+        // the max logit is pick 0's (softmax_stats' max, bitwise)
+        const float lv0 = lds_logits[lds_pick[0]];
+        const float m = lv0 == lv0 ? lv0 : -INFINITY;
+        const float ssum = softmax_sum<EJ>(lds_logits, E, lane, m);
+        const int my_id = lane < k ? lds_pick[lane] : 0;
+        const float lv = lds_logits[my_id];
+        const float my_w = pick_weight(lane < k ? (lv == lv ? lv : -INFINITY) : -INFINITY, m, ssum, k,
+                                       a.renorm != 0, lane);
         if (lane < k) {
+            int my_rank = 0;  // position among the k ids in ascending order
+            for (int q = 0; q < k; q++) my_rank += lds_pick[q] < my_id ? 1 : 0;
             lds_sel[my_rank] = my_id;
             lds_wsel[my_rank] = my_w;
             if (b == 0) {
@@ -212,8 +272,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         return e;
     };
 
-    // phase B: every load of this wavefront's gate_up tasks (at most kGateUpTasks, fused_grid_fits) and of its
-    // workgroup's down chunk (at most one), before any arithmetic
+    // phase B: every load of this wavefront's gate_up tasks (at most kGateUpTasks), before any arithmetic
     const int n_tasks = k * I;
     RawLane<GU> graw[kGateUpTasks][2];
 #pragma unroll
@@ -231,12 +290,6 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     const int cs = b / chunks_per_expert;  // the chunk's expert slot
     auto chunk_row = [&](int pass) { return (b % chunks_per_expert) * kChunkRows + 8 * wv + R * pass + drow; };
     RawLane<DN> draw[NBD];
-    if (has_chunk) {
-        const uint8_t* w = a.down + static_cast<int64_t>(expert_of(cs)) * a.down_stride;
-#pragma unroll
-        for (int p = 0; p < NBD; p++)
-            draw[p].fetch(w + static_cast<int64_t>(chunk_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
-    }
 
     // the shared expert's down rows of this workgroup's owner group, while the loads above are in flight
     float sgv = 1.0f;
@@ -267,8 +320,13 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
     }
 
-    // down: the h of the chunk's expert, its 64 row dots, the partials published
+    // down: the chunk's rows are requested only now (so far the gate_up rows had the bandwidth to themselves) and
+    // arrive while h crosses workgroups; then the h of the chunk's expert, 64 row dots, the partials published
     if (has_chunk) {
+        const uint8_t* w = a.down + static_cast<int64_t>(expert_of(cs)) * a.down_stride;
+#pragma unroll
+        for (int p = 0; p < NBD; p++)
+            draw[p].fetch(w + static_cast<int64_t>(chunk_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
         ok = gather_tagged(
                  a.sync, I, tag, [&](int i) { return kTagH + 2 * (cs * I + i); }, [&](int i) { return &lds_h[i]; }) &&
              ok;
