@@ -49,15 +49,18 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // Router for many tokens. A workgroup computes a 64-token x 64-row tile (rows: experts, then the shared gate as row
-// E); each thread 4 x 4 outputs. Per 64-value segment the operands are staged in LDS (transposed, so a thread's 4
-// tokens / 4 rows are one 16-byte read) and every output chains 64 fused multiply-adds in ascending k; the
+// E); thread (tx, ty) the 16 outputs of tokens ty + 16 i and rows tx + 16 j (i, j < 4). Per 64-value segment the
+// operands are staged in LDS row-major (64 values + 4 of padding per token or row, so the 16 rows a wavefront reads
+// at once fall in different bank groups), and every output chains 64 fused multiply-adds in ascending k; the
 // segment partial is then added to the running total: the order of router_row and of the CPU replay.
+constexpr int kRtStride = kRouterSeg + 4;
+
 __global__ __launch_bounds__(256) void k_router_tiled(const float* __restrict__ x, const float* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ shared_gate, int T, int H, int E,
                                                       float* __restrict__ logits, float* __restrict__ sg) {
-    __shared__ float xs[kRouterSeg][64];
-    __shared__ float ws[kRouterSeg][64];
+    __shared__ __attribute__((aligned(16))) float xs[64 * kRtStride];
+    __shared__ __attribute__((aligned(16))) float ws[64 * kRtStride];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int t0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
     const int rows = E + (shared_gate ? 1 : 0);
@@ -67,42 +70,56 @@ __global__ __launch_bounds__(256) void k_router_tiled(const float* __restrict__ 
 #pragma unroll
         for (int j = 0; j < 4; j++) tot[i][j] = 0.0f;
     const int nseg = H / kRouterSeg;
+    // staging: 16 threads per token / row, one float4 each (coalesced loads, conflict-free stores); segment s + 1
+    // is loaded into registers while segment s is computed
+    const int c4 = (tid & 15) * 4;
+    const float* xrow[4];
+    const float* wrow[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int rr = (tid >> 4) + 16 * q, t = t0 + rr, r = r0 + rr;
+        xrow[q] = t < T ? x + static_cast<int64_t>(t) * H + c4 : nullptr;
+        wrow[q] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + c4 : nullptr;
+    }
+    float4 xn[4], wn[4];
+    auto load_seg = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            xn[q] = xrow[q] ? *reinterpret_cast<const float4*>(xrow[q] + s * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + s * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load_seg(0);
     for (int s = 0; s < nseg; s++) {
         __syncthreads();
-        // stage: 64 tokens x 64 values and 64 rows x 64 values, transposed into [k][token] / [k][row]
-        for (int i = tid; i < 64 * 16; i += 256) {
-            const int rr = i >> 4, c4 = (i & 15) * 4;
-            const int t = t0 + rr, r = r0 + rr;
-            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < T) xv = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(t) * H + s * kRouterSeg + c4);
-            if (r < rows) {
-                const float* wr = r < E ? w + static_cast<int64_t>(r) * H : shared_gate;
-                wv = *reinterpret_cast<const float4*>(wr + s * kRouterSeg + c4);
-            }
-            xs[c4 + 0][rr] = xv.x;
-            xs[c4 + 1][rr] = xv.y;
-            xs[c4 + 2][rr] = xv.z;
-            xs[c4 + 3][rr] = xv.w;
-            ws[c4 + 0][rr] = wv.x;
-            ws[c4 + 1][rr] = wv.y;
-            ws[c4 + 2][rr] = wv.z;
-            ws[c4 + 3][rr] = wv.w;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int rr = (tid >> 4) + 16 * q;
+            *reinterpret_cast<float4*>(&xs[rr * kRtStride + c4]) = xn[q];
+            *reinterpret_cast<float4*>(&ws[rr * kRtStride + c4]) = wn[q];
         }
         __syncthreads();
+        if (s + 1 < nseg) load_seg(s + 1);
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) seg[i][j] = 0.0f;
-#pragma unroll 8
-        for (int kk = 0; kk < kRouterSeg; kk++) {
-            const float4 xv = *reinterpret_cast<const float4*>(&xs[kk][4 * ty]);
-            const float4 wv = *reinterpret_cast<const float4*>(&ws[kk][4 * tx]);
-            const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
-            const float wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll 4
+        for (int kk = 0; kk < kRouterSeg; kk += 4) {
+            float4 xv[4], wv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const float4*>(&xs[(ty + 16 * i) * kRtStride + kk]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) wv[j] = *reinterpret_cast<const float4*>(&ws[(tx + 16 * j) * kRtStride + kk]);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) seg[i][j] = __builtin_fmaf(xa[i], wa[j], seg[i][j]);
+                for (int j = 0; j < 4; j++) {
+                    seg[i][j] = __builtin_fmaf(xv[i].x, wv[j].x, seg[i][j]);
+                    seg[i][j] = __builtin_fmaf(xv[i].y, wv[j].y, seg[i][j]);
+                    seg[i][j] = __builtin_fmaf(xv[i].z, wv[j].z, seg[i][j]);
+                    seg[i][j] = __builtin_fmaf(xv[i].w, wv[j].w, seg[i][j]);
+                }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -111,11 +128,11 @@ __global__ __launch_bounds__(256) void k_router_tiled(const float* __restrict__ 
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int t = t0 + 4 * ty + i;
+        const int t = t0 + ty + 16 * i;
         if (t >= T) continue;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int r = r0 + 4 * tx + j;
+            const int r = r0 + tx + 16 * j;
             if (r < E)
                 logits[static_cast<int64_t>(t) * E + r] = bias ? __fadd_rn(tot[i][j], bias[r]) : tot[i][j];
             else if (r == E && shared_gate)
@@ -549,12 +566,29 @@ __global__ __launch_bounds__(256) void k_gemm_down(PrefillArgs a) {
 
 // ---------------------------------------------------------------------------------------------------------------
 
+// The shared gate's logit for many tokens when it would be the lone row of an extra router tile: a wavefront per
+// two tokens (one per half), router_row's order.
+__global__ __launch_bounds__(256) void k_router_sg(const float* __restrict__ x, const float* __restrict__ shared_gate,
+                                                   int T, int H, float* __restrict__ sg) {
+    const int lane = threadIdx.x & 63;
+    const int t = 2 * (blockIdx.x * 4 + (threadIdx.x >> 6)) + (lane >> 5);
+    const bool valid = t < T;
+    const float total = router_row(x + static_cast<int64_t>(valid ? t : 0) * H, shared_gate, valid, H, lane);
+    if ((lane & 31) == 0 && valid) sg[t] = sigmoid(total);
+}
+
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s) {
     const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
-    const int rows = L.n_experts + (shared_gate ? 1 : 0);
+    // with whole 64-row tiles of experts the shared gate gets its own small kernel instead of a 1-row tile
+    const bool separate = shared_gate && L.n_experts % 64 == 0;
+    const float* tiled_gate = separate ? nullptr : shared_gate;
+    const int rows = L.n_experts + (tiled_gate ? 1 : 0);
     const dim3 grid(static_cast<unsigned>((T + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
-    k_router_tiled<<<grid, 256, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden,
+    k_router_tiled<<<grid, 256, 0, s>>>(x, L.router, L.router_bias, tiled_gate, static_cast<int>(T), L.hidden,
                                         L.n_experts, logits, sg);
+    if (separate)
+        k_router_sg<<<static_cast<unsigned>((T + 7) / 8), 256, 0, s>>>(x, shared_gate, static_cast<int>(T),
+                                                                       L.hidden, sg);
     return launch_status();
 }
 
