@@ -115,8 +115,9 @@ size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Which path wl_moe_layer takes for `tokens` tokens: 1 = one fused persistent kernel (batch-1 decode at
- * Qwen3.6-like shapes), 2 = bf16 MFMA grouped expert GEMMs (prefill: tokens * top_k >= 16 * n_experts), 0 = the
- * fp32 multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an invalid layer. */
+ * Qwen3.6-like shapes), 2 = bf16 MFMA grouped expert GEMMs (more than 8 tokens: the reference's own split between
+ * its exact-weight GEMV and a bf16 matmul of dequantized weights, gguf/metal.py:20,401-408), 0 = the fp32
+ * multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an invalid layer. */
 int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens);
 
 /* Router: logits = x W_r^T (+ bias) in a fixed floating-point order: hidden is cut into segments of 64

@@ -62,9 +62,14 @@ def expert_ffn(x: np.ndarray, gate_up_w: np.ndarray, down_w: np.ndarray, inter: 
     return h @ down_w.astype(dtype).T
 
 
-def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False, return_routing: bool = False):
+def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False, return_routing: bool = False,
+          bf16_shared: bool = None):
     """The whole MoE layer for x fp32 [T, hidden]; lw is a layer dict as synth.moe_layer builds it. Returns
-    y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values)."""
+    y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values). bf16_operands
+    rounds the routed experts' operands to bf16 (expert_ffn); bf16_shared does the same for the shared expert
+    (default: as bf16_operands)."""
+    if bf16_shared is None:
+        bf16_shared = bf16_operands
     hidden, inter, experts = lw["hidden"], lw["inter"], lw["experts"]
     x = np.ascontiguousarray(x, dtype=np.float32)
     logits = cref.router_logits(x, lw["router"], lw.get("router_bias"))
@@ -81,7 +86,7 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False
         s_inter = lw["shared_inter"]
         gate_up_w = dequantize_matrix(lw["shared_gate_up"], lw["shared_gate_up_type"], 2 * s_inter, hidden)
         down_w = dequantize_matrix(lw["shared_down"], lw["shared_down_type"], hidden, s_inter)
-        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype, bf16_operands)
+        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype, bf16_shared)
         if lw.get("shared_gate") is not None:
             z = cref.router_logits(x, lw["shared_gate"][None, :])[:, 0]
             shared_gate = sigmoid(z.astype(np.float32)).astype(np.float32)

@@ -26,6 +26,8 @@ def run_layer(hip, layer, x):
 
 
 def check_layer(hip, layer, lw, x, label):
+    if layer.plan(x.shape[0]) == "mfma":  # more than 8 tokens: bf16 operands, as the reference's own split
+        return check_prefill(hip, layer, lw, x, label)
     print(f"[moe] {label}: T={x.shape[0]}", flush=True)
     y, ids, wts = run_layer(hip, layer, x)
     y_ref, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, return_routing=True)
@@ -57,7 +59,8 @@ def test_fused_matches_multi_kernel(hip, c2, layer_c2):
     """Batch-1 decode runs as one fused persistent kernel; it must give the multi-kernel path's routing bits and
     its outputs up to the compiler's multiply-add contraction in the combine (~1e-6)."""
     multi = hip.MoELayer.from_host(layer_c2, fused=False)
-    assert c2.plan(1) == "fused" and multi.plan(1) == "gemv" and c2.plan(2) == "gemv" and c2.plan(600) == "mfma"
+    assert c2.plan(1) == "fused" and multi.plan(1) == "gemv" and c2.plan(2) == "gemv" and c2.plan(8) == "gemv"
+    assert c2.plan(9) == "mfma" and c2.plan(600) == "mfma"
     for seed in range(5):
         x = synth.tokens(200 + seed, 1)
         y_f, ids_f, w_f = run_layer(hip, c2, x)
@@ -89,9 +92,24 @@ def test_layer_c2_repeatable(hip, c2, layer_c2):
     np.testing.assert_array_equal(a, b)  # no atomics in the sums: bit-identical reruns
 
 
-@pytest.mark.parametrize("T", [2, 7, 64])
+@pytest.fixture(scope="module")
+def c2_fp32(hip, layer_c2):
+    """The same layer pinned to the fp32 expert kernels at every token count."""
+    return hip.MoELayer.from_host(layer_c2, mfma="never")
+
+
+@pytest.mark.parametrize("T", [2, 7, 8, 9, 64])
 def test_layer_c2_batches(hip, c2, layer_c2, T):
+    """Up to 8 tokens the fp32 expert kernels, from 9 the bf16 MFMA GEMMs (checked against the bf16-operand
+    oracle)."""
     check_layer(hip, c2, layer_c2, synth.tokens(100 + T, T), f"c2 b={T}")
+
+
+@pytest.mark.parametrize("T", [64, 300])
+def test_layer_c2_fp32_experts(hip, c2_fp32, layer_c2, T):
+    """The fp32 expert kernels at batch sizes the default plan gives to the MFMA path."""
+    assert c2_fp32.plan(T) == "gemv"
+    check_layer(hip, c2_fp32, layer_c2, synth.tokens(100 + T, T), f"c2 fp32 b={T}")
 
 
 def test_layer_multi_chunk_sort(hip, c2, layer_c2):
@@ -104,7 +122,9 @@ def test_layer_zipf_b64(hip):
     lw = synth.moe_layer(3, zipf_alpha=1.1)
     layer = hip.MoELayer.from_host(lw)
     x = synth.tokens(33, 64)
+    assert layer.plan(64) == "mfma"
     check_layer(hip, layer, lw, x, "zipf b=64")
+    check_layer(hip, hip.MoELayer.from_host(lw, mfma="never"), lw, x, "zipf b=64 fp32")
     _, ids, _ = run_layer(hip, layer, x)
     counts = np.bincount(ids.reshape(-1), minlength=256)
     assert counts.max() >= 32  # a hot expert sees at least half the tokens

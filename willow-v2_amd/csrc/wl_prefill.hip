@@ -643,8 +643,9 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
 
 bool prefill_eligible(const WlMoeLayer& L, int64_t T) {
     if (L.flags & WL_MOE_NO_MFMA) return false;
-    if (!(L.flags & WL_MOE_FORCE_MFMA) && T * L.top_k < static_cast<int64_t>(kMfmaMinTokensPerExpert) * L.n_experts)
-        return false;
+    // the reference's own split (gguf/metal.py:20,401-408): up to MAX_TOKENS tokens its exact-weight GEMV, above
+    // that a bf16 matmul of the weights dequantized to bf16
+    if (!(L.flags & WL_MOE_FORCE_MFMA) && T <= kGemvMaxTokens) return false;
     if (L.hidden % 256 != 0 || L.inter % 128 != 0) return false;
     if (L.shared_gate_up && (L.shared_gate_up_type != L.gate_up_type || L.shared_down_type != L.down_type ||
                              L.shared_inter % 128 != 0))

@@ -86,8 +86,9 @@ class MoELayer:
         return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
 
     def plan(self, tokens: int) -> str:
-        """'fused' (one persistent kernel), 'mfma' (bf16 MFMA expert GEMMs) or 'gemv' (fp32 expert GEMVs) for this
-        many tokens."""
+        """'fused' (one persistent kernel, 1 token), 'gemv' (fp32 expert kernels, up to 8 tokens) or 'mfma' (bf16
+        MFMA expert GEMMs, more than 8: the reference's own split, gguf/metal.py:20,401-408) for this many tokens;
+        mfma='never' / 'always' at construction pins the choice."""
         return {1: "fused", 2: "mfma", 0: "gemv"}[library().wl_moe_plan(ctypes.byref(self.struct), tokens)]
 
     def workspace(self, tokens: int) -> torch.Tensor:
