@@ -39,8 +39,11 @@ def check_layer(hip, layer, lw, x, label):
     return err
 
 
-def test_route_c2(hip, c2, layer_c2):
-    x = synth.tokens(2, 64)
+@pytest.mark.parametrize("T", [1, 2, 9, 64, 300, 1000])
+def test_route_c2(hip, c2, layer_c2, T):
+    """Routing bits at token counts that take each router kernel (one token, the per-row GEMV over token
+    groups, the tiled kernel)."""
+    x = synth.tokens(2, T)
     wts, ids, sg = c2.route(torch.from_numpy(x).cuda())
     logits = cref.router_logits(x, layer_c2["router"])
     w_ref, ids_ref = moe_ref.route(logits, 8, True)

@@ -14,70 +14,62 @@ namespace wl {
 // Router. logits[t, e] = x[t] . W[e] (+ bias[e]) in a fixed order the CPU oracle replays exactly:
 //   k is cut into segments of kRouterSeg consecutive values; each segment's partial is a chain of fused
 //   multiply-adds in ascending k starting from 0; the partials are added left to right; then the bias.
-// Decode mapping: 32 lanes per row (lane s owns segments s, s+32, ...), two rows per wavefront, TT tokens per pass.
+// Small batches (2 tokens up to the tiled kernel's minimum): a workgroup of 256 threads covers 8 rows x TT tokens.
+// Wavefront w owns rows 2w and 2w + 1, 32 lanes per row; lane s owns segments s, s + 32, ..., loads each segment's
+// 64 weights once and chains the TT tokens' partials from them. The partials go to LDS; then thread (token u,
+// row r) adds its output's partials left to right. A ragged last token group recomputes its last token for the
+// missing ones and stores nothing for them.
 // The shared-expert gate is row E (weight vector shared_gate, no bias); its output is sigmoid(logit).
 template <int TT>
-__global__ __launch_bounds__(64) void k_router(const float* __restrict__ x, const float* __restrict__ w,
-                                               const float* __restrict__ bias,
-                                               const float* __restrict__ shared_gate, int T, int H, int E,
-                                               float* __restrict__ logits, float* __restrict__ sg) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 2 + (lane >> 5);
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ w,
+                                                const float* __restrict__ bias,
+                                                const float* __restrict__ shared_gate, int T, int H, int E,
+                                                float* __restrict__ logits, float* __restrict__ sg) {
+    extern __shared__ float part[];  // [8 rows][TT tokens][nseg + 1]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int rl = 2 * (tid >> 6) + (lane >> 5);
+    const int row = blockIdx.x * 8 + rl;
     const int slot = lane & 31;
     const int rows_total = E + (shared_gate ? 1 : 0);
     const bool valid = row < rows_total;
-    const float* wr = row < E ? w + static_cast<int64_t>(row) * H : shared_gate;
-    const int nseg = H / kRouterSeg;
-    const int src_base = lane & 32;
-    for (int t0 = 0; t0 < T; t0 += TT) {
-        float p[kRouterMaxJ][TT];
+    const float* wr = valid ? (row < E ? w + static_cast<int64_t>(row) * H : shared_gate) : w;
+    const int nseg = H / kRouterSeg, stride = nseg + 1;
+    const int t0 = blockIdx.y * TT;
+    const float* xt[TT];
 #pragma unroll
-        for (int j = 0; j < kRouterMaxJ; j++)
+    for (int u = 0; u < TT; u++) xt[u] = x + static_cast<int64_t>(min(t0 + u, T - 1)) * H;
+    for (int s = slot; s < nseg; s += 32) {
+        float p[TT];
 #pragma unroll
-            for (int u = 0; u < TT; u++) p[j][u] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kRouterMaxJ; j++) {
-            const int s = slot + 32 * j;
-            if (valid && s < nseg) {
-                const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
+        for (int u = 0; u < TT; u++) p[u] = 0.0f;
+        const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
 #pragma unroll 4
-                for (int i = 0; i < kRouterSeg / 4; i++) {
-                    const float4 wv = wp[i];
+        for (int i = 0; i < kRouterSeg / 4; i++) {
+            const float4 wv = wp[i];
 #pragma unroll
-                    for (int u = 0; u < TT; u++) {
-                        if (t0 + u < T) {
-                            const float4 xv = *reinterpret_cast<const float4*>(
-                                x + static_cast<int64_t>(t0 + u) * H + s * kRouterSeg + 4 * i);
-                            p[j][u] = __builtin_fmaf(xv.x, wv.x, p[j][u]);
-                            p[j][u] = __builtin_fmaf(xv.y, wv.y, p[j][u]);
-                            p[j][u] = __builtin_fmaf(xv.z, wv.z, p[j][u]);
-                            p[j][u] = __builtin_fmaf(xv.w, wv.w, p[j][u]);
-                        }
-                    }
-                }
+            for (int u = 0; u < TT; u++) {
+                const float4 xv = *reinterpret_cast<const float4*>(xt[u] + s * kRouterSeg + 4 * i);
+                p[u] = __builtin_fmaf(xv.x, wv.x, p[u]);
+                p[u] = __builtin_fmaf(xv.y, wv.y, p[u]);
+                p[u] = __builtin_fmaf(xv.z, wv.z, p[u]);
+                p[u] = __builtin_fmaf(xv.w, wv.w, p[u]);
             }
         }
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            float total = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kRouterMaxJ; j++) {
-                if (32 * j < nseg) {
-                    for (int sl = 0; sl < 32; sl++) {
-                        const int s = sl + 32 * j;
-                        if (s < nseg) {
-                            const float v = __shfl(p[j][u], src_base + sl);
-                            total = s == 0 ? v : __fadd_rn(total, v);
-                        }
-                    }
-                }
-            }
-            if (slot == 0 && valid && t0 + u < T) {
-                if (row < E)
-                    logits[static_cast<int64_t>(t0 + u) * E + row] = bias ? __fadd_rn(total, bias[row]) : total;
-                else
-                    sg[t0 + u] = sigmoid(total);
-            }
+        for (int u = 0; u < TT; u++) part[(rl * TT + u) * stride + s] = p[u];
+    }
+    __syncthreads();
+    if (tid < 8 * TT) {
+        const int u = tid >> 3, r = tid & 7;  // 8 consecutive rows of one token: contiguous stores
+        const int rr = blockIdx.x * 8 + r, t = t0 + u;
+        if (t < T && rr < rows_total) {
+            const float* pp = part + (r * TT + u) * stride;
+            float total = pp[0];
+            for (int q = 1; q < nseg; q++) total = __fadd_rn(total, pp[q]);
+            if (rr < E)
+                logits[static_cast<int64_t>(t) * E + rr] = bias ? __fadd_rn(total, bias[rr]) : total;
+            else
+                sg[t] = sigmoid(total);
         }
     }
 }
@@ -562,9 +554,17 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
     const int grid = (rows + 1) / 2;
     if (T == 1)
         k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
-    else
-        k_router<8><<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden,
-                                         L.n_experts, logits, sg);
+    else {
+        // partials in LDS: 8 rows x TT tokens x (segments + 1) floats, at most 33 KiB
+        const int stride = L.hidden / kRouterSeg + 1;
+        const unsigned rgrid = static_cast<unsigned>((rows + 7) / 8);
+        if (stride <= 129)
+            k_router<8><<<dim3(rgrid, static_cast<unsigned>((T + 7) / 8)), 256, 8 * 8 * stride * 4, s>>>(
+                x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
+        else
+            k_router<4><<<dim3(rgrid, static_cast<unsigned>((T + 3) / 4)), 256, 8 * 4 * stride * 4, s>>>(
+                x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
+    }
     return launch_status();
 }
 
@@ -735,7 +735,8 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
     if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16) return WL_EINVAL_ALIGN;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    rc = launch_router(*layer, x, tokens, logits, shared_gate_out, s);
+    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(*layer, x, tokens, logits, shared_gate_out, s)
+                                         : launch_router(*layer, x, tokens, logits, shared_gate_out, s);
     if (rc) return rc;
     return launch_topk(*layer, logits, tokens, ids, weights, nullptr, s);
 }

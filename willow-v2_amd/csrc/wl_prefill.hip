@@ -13,7 +13,7 @@
 //   k_gemm_down      per (tile, 256 output rows): o = down h, fp32, by sorted position (combined by k_combine)
 //
 // MFMA 16x16x32 bf16 operand layout (wave64): lane l holds A[l % 16][8 (l / 16) + i], B[8 (l / 16) + i][l % 16],
-// and C[4 (l / 16) + i][l % 16], i < 8 (A, B) or < 4 (C). A wavefront covers 4 row tiles x 8 token tiles.
+// and C[4 (l / 16) + i][l % 16], i < 8 (A, B) or < 4 (C). A wavefront covers kRT row tiles x 8 token tiles.
 #include <hip/hip_runtime.h>
 
 #include "wl_common.h"
@@ -29,6 +29,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kBK = 256;              // k per staged chunk: one K-quant block per row
 constexpr int kTileRowBytes = kBK * 2;                     // one token's chunk in LDS: 512 bytes, 32 slots of 16
 constexpr int kTileBytes = kTileTokens * kTileRowBytes;     // 64 KiB per buffer
+// A GEMM workgroup covers 16 row tiles of 16 rows against one token tile: kGemmWaves wavefronts of kRT row tiles
+// each. Two row tiles per wavefront keep a wavefront within 256 registers, so the 8 wavefronts of a workgroup run
+// two per SIMD and one's dequantization overlaps the other's waits.
+constexpr int kRT = 2;
+constexpr int kGemmWaves = 16 / kRT;
+constexpr int kGemmThreads = 64 * kGemmWaves;
 
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -328,11 +334,11 @@ constexpr bool kSchedGroups = false;
 // step) and, as each b[n] has been consumed, reading step KK + 1's b[n] in its place (the last step's successor
 // reads from the other LDS buffer after the barrier), so the decode runs while the matrix core is busy.
 template <int TYPE, int NT, int KK>
-__device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const RowState<TYPE> (&rs)[4],
-                                          const RowState<TYPE> (&nx)[4], floatx4 (&acc)[4][8], const bf16x8 (&a)[4],
-                                          bf16x8 (&b)[8], bf16x8 (&an)[4], int q) {
+__device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const RowState<TYPE> (&rs)[kRT],
+                                          const RowState<TYPE> (&nx)[kRT], floatx4 (&acc)[kRT][8],
+                                          const bf16x8 (&a)[kRT], bf16x8 (&b)[8], bf16x8 (&an)[kRT], int q) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kRT; r++) {
         if constexpr (KK < 7)
             an[r] = rs[r].template frag<KK + 1>(q);
         else
@@ -341,15 +347,15 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const Ro
 #pragma unroll
     for (int n = 0; n < NT; n++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < kRT; r++)
             acc[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r], b[n], acc[r][n], 0, 0, 0);
         if constexpr (KK < 7) b[n] = read_b1<KK + 1>(buf, ba, n);
     }
     if constexpr (kSchedGroups) {
-        // 4 NT MFMAs per step against ~120 VALU instructions of decode
+        // kRT NT MFMAs per step against ~34 kRT VALU instructions of decode
         constexpr int kValuPer = NT == 8 ? 4 : 8;
 #pragma unroll
-        for (int i = 0; i < 4 * NT; i++) {
+        for (int i = 0; i < kRT * NT; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (KK < 7 && (i & 3) == 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
@@ -358,15 +364,20 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const Ro
 }
 
 // Direct global -> LDS staging of a K chunk with gfx950's global_load_lds_dwordx4: one wavefront instruction writes
-// 64 consecutive 16-byte LDS slots (M0 + 16 lane), two token rows. Instruction `it` of wavefront w fills rows
-// 8 it + 2 w + (lane >> 5); lane slot s = lane & 31 of row t takes the 16 bytes of values 8 (s ^ (t & 7)) .. + 7,
-// and t & 7 = 2 w + (lane >> 5) does not depend on it, so the lane's byte column `col` is fixed. The rows' byte
-// offsets come from `rowtab`, laid out so that a lane's 16 are contiguous: rowtab[16 (t & 7) + (t >> 3)].
+// 64 consecutive 16-byte LDS slots (M0 + 16 lane), two token rows. With W = kGemmWaves, instruction `it` of
+// wavefront w fills rows 2 W it + 2 w + (lane >> 5); lane slot s = lane & 31 of row t takes the 16 bytes of values
+// 8 (s ^ (t & 7)) .. + 7, and t & 7 = (2 w + (lane >> 5)) & 7 does not depend on it (2 W is a multiple of 8), so
+// the lane's byte column `col` is fixed. The rows' byte offsets come from `rowtab`, laid out so that a lane's
+// kStageIters are contiguous: rowtab[kStageIters (t % 2 W) + t / 2 W].
 //
 // The loads are issued from inline assembly so that the compiler, which cannot tell the two LDS buffers apart,
 // does not wait for them before the next LDS read of the other buffer; the K loop waits for them itself
 // (s_waitcnt vmcnt(0) and a barrier) before the buffer is read.
-constexpr int kStageIters = kTileBytes / (4 * 1024);  // 16
+constexpr int kStageIters = kTileBytes / (kGemmWaves * 1024);  // 8
+static_assert(kGemmWaves % 4 == 0 && kStageIters % 4 == 0 && kTileTokens == 2 * kGemmWaves * kStageIters, "");
+__host__ __device__ constexpr int rowtab_index(int t) {
+    return kStageIters * (t % (2 * kGemmWaves)) + t / (2 * kGemmWaves);
+}
 
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
@@ -374,10 +385,10 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 
 __device__ __forceinline__ void stage_async(uint32_t buf, const uint8_t* src, const uint32_t* rowtab, uint32_t col,
                                             int wv, int half) {
-    const uint4* tab = reinterpret_cast<const uint4*>(rowtab + 16 * (2 * wv + half));
-    uint32_t off[16];
+    const uint4* tab = reinterpret_cast<const uint4*>(rowtab + kStageIters * (2 * wv + half));
+    uint32_t off[kStageIters];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < kStageIters / 4; i++) {
         const uint4 v = tab[i];
         off[4 * i] = v.x;
         off[4 * i + 1] = v.y;
@@ -391,7 +402,7 @@ __device__ __forceinline__ void stage_async(uint32_t buf, const uint8_t* src, co
         asm volatile(
             "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
             : "=&s"(saved)
-            : "s"(buf + (4 * it + wv) * 1024), "v"(off[it] + col), "s"(src)
+            : "s"(buf + (kGemmWaves * it + wv) * 1024), "v"(off[it] + col), "s"(src)
             : "memory");
     }
 }
@@ -412,26 +423,26 @@ __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 // the last iteration requests the row states of its own block again (keeping the loop free of branches around the
 // register loads) and no tile.
 template <int TYPE, int NT, typename RowPtr>
-__device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[4][8], int nblocks,
+__device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[kRT][8], int nblocks,
                                           const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr, int lr, int q) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
     const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
     const uint32_t lds0 = lds_address(bufs[0]), lds1 = lds_address(bufs[1]);
     const BAddr ba = b_addr(lr, q);
-    RowState<TYPE> rs[4], nx[4];
+    RowState<TYPE> rs[kRT], nx[kRT];
 #pragma unroll
-    for (int r = 0; r < 4; r++) rs[r].fetch(row_ptr(r, lr), q);
+    for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr), q);
     stage_async(lds0, src, rowtab, col, wv, half);
-    bf16x8 a0[4], a1[4], b[8];
+    bf16x8 a0[kRT], a1[kRT], b[8];
 #pragma unroll
-    for (int r = 0; r < 4; r++) a0[r] = rs[r].template frag<0>(q);
+    for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
     for (int kc = 0; kc < nblocks; kc++) {
         wait_stage();     // this chunk's LDS tile has landed
         __syncthreads();  // ... for every wavefront, and the other buffer is free
         const int kn = kc + 1 < nblocks ? kc + 1 : kc;
 #pragma unroll
-        for (int r = 0; r < 4; r++) nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
+        for (int r = 0; r < kRT; r++) nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
         if (kc + 1 < nblocks) stage_async((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
                                           rowtab, col, wv, half);
         const uint8_t* buf = bufs[kc & 1];
@@ -445,27 +456,27 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
         gemm_step<TYPE, NT, 6>(buf, ba, rs, nx, acc, a0, b, a1, q);
         gemm_step<TYPE, NT, 7>(buf, ba, rs, nx, acc, a1, b, a0, q);
 #pragma unroll
-        for (int r = 0; r < 4; r++) rs[r] = nx[r];
+        for (int r = 0; r < kRT; r++) rs[r] = nx[r];
     }
     wait_stage();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// The GEMM core: a workgroup of 4 wavefronts, each owning 4 row tiles of 16 (rows given by row_ptr(r, lr)) and the
-// tile's (up to) 128 tokens as 8 token tiles (4 when the tile has at most 64 tokens). Per K chunk of 256 values (one
-// block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes 4 A-fragments
-// and runs 4 x NT MFMAs. src_row(t) is token t's row in src ([*, ld] bf16); rows past count load token 0's (their
+// The GEMM core: a workgroup of kGemmWaves wavefronts, each owning kRT row tiles of 16 (rows given by
+// row_ptr(r, lr)) and the tile's (up to) 128 tokens as 8 token tiles (4 when the tile has at most 64 tokens). Per K
+// chunk of 256 values (one block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value
+// steps decodes kRT A-fragments and runs kRT x NT MFMAs. src_row(t) is token t's row in src ([*, ld] bf16); rows past count load token 0's (their
 // results are never stored).
 template <int TYPE, typename RowPtr, typename SrcRow>
-__device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[4][8], int nblocks,
+__device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[kRT][8], int nblocks,
                                           int count, const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
                                           RowPtr row_ptr) {
     __shared__ __attribute__((aligned(16))) uint32_t rowtab[kTileTokens];
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     for (int t = threadIdx.x; t < kTileTokens; t += blockDim.x)
-        rowtab[16 * (t & 7) + (t >> 3)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
+        rowtab[rowtab_index(t)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < kRT; r++)
 #pragma unroll
         for (int n = 0; n < 8; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();
@@ -487,10 +498,10 @@ __device__ __forceinline__ void slab_tile(int nslab, int& slab, int& tile) {
     tile = (i / nslab) * kXcds + x;
 }
 
-// gate_up: slab = 128-row slab of the intermediate dim; wavefront w: gate rows j0 + 16r + lr (r = 0, 1)
-// and the matching up rows inter + j0 + ... (r = 2, 3), j0 = 128 slab + 32 w. Epilogue h = silu(g) * u -> bf16.
+// gate_up: slab = 128-row slab of the intermediate dim; wavefront w: gate rows j0 + 16r + lr (r < kRT / 2)
+// and the matching up rows inter + j0 + ... (r >= kRT / 2), j0 = 128 slab + 8 kRT w. Epilogue h = silu(g) * u -> bf16.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
     int slab, ti;
     slab_tile(a.nslab_gate_up, slab, ti);
@@ -498,29 +509,30 @@ __global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
     const int4 tile = a.tiles[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
-    const int j0 = slab * 128 + 32 * (threadIdx.x >> 6);
+    constexpr int kHalf = kRT / 2;
+    const int j0 = slab * 128 + 16 * kHalf * (threadIdx.x >> 6);
     if (slab * 128 >= inter) return;
     const uint8_t* W = sh ? a.sh_gate_up : a.gate_up + static_cast<int64_t>(tile.x) * a.gate_up_stride;
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
-    floatx4 acc[4][8];
+    floatx4 acc[kRT][8];
     auto row_ptr = [&](int r, int lr) {
-        const int j = j0 + 16 * (r & 1) + lr;
-        return W + static_cast<int64_t>((r < 2 ? 0 : inter) + j) * rs;
+        const int j = j0 + 16 * (r % kHalf) + lr;
+        return W + static_cast<int64_t>((r < kHalf ? 0 : inter) + j) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
     gemm_tile<TYPE>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     uint16_t* out = sh ? a.h_sh16 : a.h16;
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
+    for (int r = 0; r < kHalf; r++) {
 #pragma unroll
         for (int n = 0; n < 8; n++) {
             const int t = 16 * n + lr;
             if (t < count) {
                 const int j = j0 + 16 * r + 4 * q;
-                const floatx4 g = acc[r][n], u = acc[r + 2][n];
+                const floatx4 g = acc[r][n], u = acc[r + kHalf][n];
                 const uint2 v = make_uint2(pack2(silu(g[0]) * u[0], silu(g[1]) * u[1]),
                                            pack2(silu(g[2]) * u[2], silu(g[3]) * u[3]));
                 *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j) = v;
@@ -529,9 +541,9 @@ __global__ __launch_bounds__(256) void k_gemm_gate_up(PrefillArgs a) {
     }
 }
 
-// down: slab = 256-row slab of the hidden dim; wavefront w: rows r0 + 64 w + 16 r + lr. o fp32 by position.
+// down: slab = 256-row slab of the hidden dim; wavefront w: rows r0 + 16 kRT w + 16 r + lr. o fp32 by position.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_gemm_down(PrefillArgs a) {
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
     int slab, ti;
     slab_tile(a.H / 256, slab, ti);
@@ -539,19 +551,19 @@ __global__ __launch_bounds__(256) void k_gemm_down(PrefillArgs a) {
     const int4 tile = a.tiles[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
-    const int row0 = slab * 256 + 64 * (threadIdx.x >> 6);
+    const int row0 = slab * 256 + 16 * kRT * (threadIdx.x >> 6);
     const uint8_t* W = sh ? a.sh_down : a.down + static_cast<int64_t>(tile.x) * a.down_stride;
     const int nb = inter / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
-    floatx4 acc[4][8];
+    floatx4 acc[kRT][8];
     auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>(row0 + 16 * r + lr) * rs; };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
     gemm_tile<TYPE>(bufs, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     float* out = sh ? a.o_sh : a.o;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < kRT; r++) {
 #pragma unroll
         for (int n = 0; n < 8; n++) {
             const int t = 16 * n + lr;
@@ -630,14 +642,14 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     const dim3 g1(static_cast<unsigned>(a.nslab_gate_up * tiles8));
     // the routed and shared experts share one launch, so their types must agree (checked by prefill_eligible)
     if (L.gate_up_type == WL_TYPE_Q4_K)
-        k_gemm_gate_up<WL_TYPE_Q4_K><<<g1, 256, 0, s>>>(a);
+        k_gemm_gate_up<WL_TYPE_Q4_K><<<g1, kGemmThreads, 0, s>>>(a);
     else
-        k_gemm_gate_up<WL_TYPE_Q6_K><<<g1, 256, 0, s>>>(a);
+        k_gemm_gate_up<WL_TYPE_Q6_K><<<g1, kGemmThreads, 0, s>>>(a);
     const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8));
     if (L.down_type == WL_TYPE_Q4_K)
-        k_gemm_down<WL_TYPE_Q4_K><<<g2, 256, 0, s>>>(a);
+        k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
     else
-        k_gemm_down<WL_TYPE_Q6_K><<<g2, 256, 0, s>>>(a);
+        k_gemm_down<WL_TYPE_Q6_K><<<g2, kGemmThreads, 0, s>>>(a);
     return launch_status();
 }
 
