@@ -54,7 +54,7 @@ struct ExpertArgs {
 
 constexpr int kTileTokens = 128;             // prefill: tokens per GEMM tile
 constexpr int kGemvMaxTokens = 8;  // fp32 GEMV experts up to this many tokens, bf16 MFMA GEMMs above (gguf/metal.py:20)
-constexpr int kTiledRouterMinTokens = 256;   // router as a tiled kernel from this many tokens
+constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
 
 struct PrefillArgs {
     const uint8_t* gate_up;

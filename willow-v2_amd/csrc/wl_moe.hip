@@ -14,58 +14,79 @@ namespace wl {
 // Router. logits[t, e] = x[t] . W[e] (+ bias[e]) in a fixed order the CPU oracle replays exactly:
 //   k is cut into segments of kRouterSeg consecutive values; each segment's partial is a chain of fused
 //   multiply-adds in ascending k starting from 0; the partials are added left to right; then the bias.
-// Small batches (2 tokens up to the tiled kernel's minimum): a workgroup of 256 threads covers 8 rows x TT tokens.
-// Wavefront w owns rows 2w and 2w + 1, 32 lanes per row; lane s owns segments s, s + 32, ..., loads each segment's
-// 64 weights once and chains the TT tokens' partials from them. The partials go to LDS; then thread (token u,
-// row r) adds its output's partials left to right. A ragged last token group recomputes its last token for the
-// missing ones and stores nothing for them.
+// Small batches (2 tokens up to the tiled kernel's minimum): a workgroup of 256 threads covers 16 rows x TT
+// tokens. The hidden dim is taken 16 segments at a time: the TT tokens' values of the chunk are staged in LDS with
+// coalesced loads (each 64-value segment padded to 68 floats, so that the 16 lanes reading 16 segments at once
+// spread over the banks), and lane (row 4 w + lane / 16, segment j = lane % 16) chains the TT tokens' partials of
+// segment 16 c + j from its row's 64 weights, loaded once. The partials go to LDS; thread (token u, row r) then
+// adds the chunk's partials to its output's running total, left to right. A ragged last token group recomputes its
+// last token for the missing ones and stores nothing for them.
 // The shared-expert gate is row E (weight vector shared_gate, no bias); its output is sigmoid(logit).
+constexpr int kRouterChunkSegs = 16;
+constexpr int kRouterPad = kRouterSeg + 4;
+
 template <int TT>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ w,
                                                 const float* __restrict__ bias,
                                                 const float* __restrict__ shared_gate, int T, int H, int E,
                                                 float* __restrict__ logits, float* __restrict__ sg) {
-    extern __shared__ float part[];  // [8 rows][TT tokens][nseg + 1]
+    __shared__ __attribute__((aligned(16))) float xs[TT][kRouterChunkSegs * kRouterPad];
+    __shared__ float part[16 * TT][kRouterChunkSegs + 1];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int rl = 2 * (tid >> 6) + (lane >> 5);
-    const int row = blockIdx.x * 8 + rl;
-    const int slot = lane & 31;
+    const int rl = 4 * (tid >> 6) + (lane >> 4), j = lane & 15;
+    const int row = blockIdx.x * 16 + rl;
     const int rows_total = E + (shared_gate ? 1 : 0);
-    const bool valid = row < rows_total;
-    const float* wr = valid ? (row < E ? w + static_cast<int64_t>(row) * H : shared_gate) : w;
-    const int nseg = H / kRouterSeg, stride = nseg + 1;
+    const float* wr = row < rows_total ? (row < E ? w + static_cast<int64_t>(row) * H : shared_gate) : w;
+    const int nseg = H / kRouterSeg;
     const int t0 = blockIdx.y * TT;
-    const float* xt[TT];
+    // summing thread: token su, row sr
+    const int su = tid >> 4, sr = tid & 15;
+    float total = 0.0f;
+    for (int c = 0; c < nseg; c += kRouterChunkSegs) {
+        __syncthreads();  // the previous chunk's xs and part have been read
 #pragma unroll
-    for (int u = 0; u < TT; u++) xt[u] = x + static_cast<int64_t>(min(t0 + u, T - 1)) * H;
-    for (int s = slot; s < nseg; s += 32) {
-        float p[TT];
+        for (int it = 0; it < TT; it++) {
+            const int f = tid + 256 * it;  // float4 f of the chunk: token f / 256, segment (f / 16) % 16, i = f % 16
+            const int u = f >> 8, sg4 = (f >> 4) & 15, i = f & 15;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c + sg4 < nseg)
+                v = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(min(t0 + u, T - 1)) * H +
+                                                     (c + sg4) * kRouterSeg + 4 * i);
+            *reinterpret_cast<float4*>(&xs[u][sg4 * kRouterPad + 4 * i]) = v;
+        }
+        __syncthreads();
+        if (c + j < nseg) {
+            float p[TT];
 #pragma unroll
-        for (int u = 0; u < TT; u++) p[u] = 0.0f;
-        const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
+            for (int u = 0; u < TT; u++) p[u] = 0.0f;
+            const float4* wp = reinterpret_cast<const float4*>(wr + (c + j) * kRouterSeg);
 #pragma unroll 4
-        for (int i = 0; i < kRouterSeg / 4; i++) {
-            const float4 wv = wp[i];
+            for (int i = 0; i < kRouterSeg / 4; i++) {
+                const float4 wv = wp[i];
 #pragma unroll
-            for (int u = 0; u < TT; u++) {
-                const float4 xv = *reinterpret_cast<const float4*>(xt[u] + s * kRouterSeg + 4 * i);
-                p[u] = __builtin_fmaf(xv.x, wv.x, p[u]);
-                p[u] = __builtin_fmaf(xv.y, wv.y, p[u]);
-                p[u] = __builtin_fmaf(xv.z, wv.z, p[u]);
-                p[u] = __builtin_fmaf(xv.w, wv.w, p[u]);
+                for (int u = 0; u < TT; u++) {
+                    const float4 xv = *reinterpret_cast<const float4*>(&xs[u][j * kRouterPad + 4 * i]);
+                    p[u] = __builtin_fmaf(xv.x, wv.x, p[u]);
+                    p[u] = __builtin_fmaf(xv.y, wv.y, p[u]);
+                    p[u] = __builtin_fmaf(xv.z, wv.z, p[u]);
+                    p[u] = __builtin_fmaf(xv.w, wv.w, p[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < TT; u++) part[rl * TT + u][j] = p[u];
+        }
+        __syncthreads();
+        if (tid < 16 * TT) {
+            const int n = min(kRouterChunkSegs, nseg - c);
+            for (int q = 0; q < n; q++) {
+                const float v = part[sr * TT + su][q];
+                total = (c == 0 && q == 0) ? v : __fadd_rn(total, v);
             }
         }
-#pragma unroll
-        for (int u = 0; u < TT; u++) part[(rl * TT + u) * stride + s] = p[u];
     }
-    __syncthreads();
-    if (tid < 8 * TT) {
-        const int u = tid >> 3, r = tid & 7;  // 8 consecutive rows of one token: contiguous stores
-        const int rr = blockIdx.x * 8 + r, t = t0 + u;
+    if (tid < 16 * TT) {
+        const int rr = blockIdx.x * 16 + sr, t = t0 + su;  // 16 consecutive rows of one token: contiguous stores
         if (t < T && rr < rows_total) {
-            const float* pp = part + (r * TT + u) * stride;
-            float total = pp[0];
-            for (int q = 1; q < nseg; q++) total = __fadd_rn(total, pp[q]);
             if (rr < E)
                 logits[static_cast<int64_t>(t) * E + rr] = bias ? __fadd_rn(total, bias[rr]) : total;
             else
@@ -554,17 +575,9 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
     const int grid = (rows + 1) / 2;
     if (T == 1)
         k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
-    else {
-        // partials in LDS: 8 rows x TT tokens x (segments + 1) floats, at most 33 KiB
-        const int stride = L.hidden / kRouterSeg + 1;
-        const unsigned rgrid = static_cast<unsigned>((rows + 7) / 8);
-        if (stride <= 129)
-            k_router<8><<<dim3(rgrid, static_cast<unsigned>((T + 7) / 8)), 256, 8 * 8 * stride * 4, s>>>(
-                x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
-        else
-            k_router<4><<<dim3(rgrid, static_cast<unsigned>((T + 3) / 4)), 256, 8 * 4 * stride * 4, s>>>(
-                x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
-    }
+    else
+        k_router<8><<<dim3(static_cast<unsigned>((rows + 15) / 16), static_cast<unsigned>((T + 7) / 8)), 256, 0, s>>>(
+            x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
     return launch_status();
 }
 

@@ -333,6 +333,11 @@ constexpr bool kSchedGroups = false;
 // with decoding step KK + 1's A-fragments into `an` (from `nx`, the next block's rows, when KK is the chunk's last
 // step) and, as each b[n] has been consumed, reading step KK + 1's b[n] in its place (the last step's successor
 // reads from the other LDS buffer after the barrier), so the decode runs while the matrix core is busy.
+// The first A-fragments of a block are decoded at the top of its iteration (after the barrier that follows the wait
+// for every outstanding load) rather than in the previous iteration's last step, so the row-state loads have a whole
+// iteration to land instead of seven steps.
+constexpr bool kLateFirst = true;
+
 template <int TYPE, int NT, int KK>
 __device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const RowState<TYPE> (&rs)[kRT],
                                           const RowState<TYPE> (&nx)[kRT], floatx4 (&acc)[kRT][8],
@@ -341,7 +346,7 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const Ro
     for (int r = 0; r < kRT; r++) {
         if constexpr (KK < 7)
             an[r] = rs[r].template frag<KK + 1>(q);
-        else
+        else if constexpr (!kLateFirst)
             an[r] = nx[r].template frag<0>(q);
     }
 #pragma unroll
@@ -435,8 +440,10 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
     for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr), q);
     stage_async(lds0, src, rowtab, col, wv, half);
     bf16x8 a0[kRT], a1[kRT], b[8];
+    if constexpr (!kLateFirst) {
 #pragma unroll
-    for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
+        for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
+    }
     for (int kc = 0; kc < nblocks; kc++) {
         wait_stage();     // this chunk's LDS tile has landed
         __syncthreads();  // ... for every wavefront, and the other buffer is free
@@ -447,6 +454,10 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
                                           rowtab, col, wv, half);
         const uint8_t* buf = bufs[kc & 1];
         read_b<NT, 0>(buf, ba, b);
+        if constexpr (kLateFirst) {
+#pragma unroll
+            for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
+        }
         gemm_step<TYPE, NT, 0>(buf, ba, rs, nx, acc, a0, b, a1, q);
         gemm_step<TYPE, NT, 1>(buf, ba, rs, nx, acc, a1, b, a0, q);
         gemm_step<TYPE, NT, 2>(buf, ba, rs, nx, acc, a0, b, a1, q);
