@@ -198,17 +198,42 @@ __global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offse
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// A-operand decoders: the 8 values k = 32*kk + 8*q + i (i < 8) of one row's K-quant block as bf16, for every kk of
-// the block. The per-block state is fetched once (fetch), then each kk is unpacked (fragment).
+// A-operand decoders. At 32-value step KK of a 256-value block, lane group q (lanes 16 q .. 16 q + 15, one row
+// each) supplies 8 of the step's 32 k-values; which 8 is the type's K order (k_slot below), and the B-operand is
+// read from LDS in the same order, so the product is the block's dot product with the matrix core's additions in
+// another order. The per-block state is fetched once (fetch), prepared once the loads have landed (prepare), then
+// each step is unpacked (frag).
+//
+// Q4_K order: step KK, group q holds values 32 (2 q + (KK & 1)) + 8 (KK >> 1) + i of the block, the (KK >> 1)-th 8
+// values of sub-block 2 q + (KK & 1). A group so only needs the scales of sub-blocks 2 q and 2 q + 1, whose 64 values
+// are the low and high nibbles of qs bytes 32 q .. 32 q + 31.
 struct Q4KRowState {
-    uint4 hd;      // d, dmin, 12 scale bytes
-    uint2 qs[4];   // qs bytes 32m + 8q .. +7, m < 4
+    uint4 hd;       // d, dmin, 12 scale bytes
+    uint4 qs[2];    // qs bytes 32 q .. 32 q + 31
+    float a[2], b[2];  // value = a[e] * nibble + b[e] for sub-block 2 q + e
 };
 
 __device__ __forceinline__ void fetch_q4k(const uint8_t* __restrict__ blk, int q, Q4KRowState& s) {
     s.hd = *reinterpret_cast<const uint4*>(blk);
+    s.qs[0] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * q);
+    s.qs[1] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * q);
+}
+
+// The scales of sub-blocks j = 2 q + e (q4k_scale_min with a per-lane j): j < 4 for q < 2, j >= 4 otherwise, and
+// the byte holding j's fields sits 8 ((2 q + e) & 3) bits into its word either way.
+__device__ __forceinline__ void prepare_q4k(Q4KRowState& s, int q) {
+    const float d = half_to_float(s.hd.x), dmin = half_to_float(s.hd.x >> 16);
+    const bool hi = q >= 2;
+    const uint32_t sh0 = 16u * static_cast<uint32_t>(q & 1);
 #pragma unroll
-    for (int m = 0; m < 4; m++) s.qs[m] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * m + 8 * q);
+    for (int e = 0; e < 2; e++) {
+        const uint32_t sh = sh0 + 8u * e;
+        const uint32_t s0 = s.hd.y >> sh, s1 = s.hd.z >> sh, s2 = s.hd.w >> sh;
+        const uint32_t sc = hi ? ((s2 & 0xFu) | ((s0 >> 2) & 0x30u)) : (s0 & 63u);
+        const uint32_t m = hi ? (((s2 >> 4) & 0xFu) | ((s1 >> 2) & 0x30u)) : (s1 & 63u);
+        s.a[e] = d * static_cast<float>(sc);
+        s.b[e] = -(dmin * static_cast<float>(m));
+    }
 }
 
 // v & 0x0F0F0F0F as an opaque value, so the byte conversions below stay single v_cvt_f32_ubyteN instructions
@@ -226,19 +251,18 @@ __device__ __forceinline__ void affine4(uint32_t w, float a, float b, uint32_t& 
 
 template <int KK>
 __device__ __forceinline__ bf16x8 fragment_q4k(const Q4KRowState& s) {
-    const float d = half_to_float(s.hd.x), dmin = half_to_float(s.hd.x >> 16);
-    uint32_t sc, m;
-    q4k_scale_min(KK, s.hd.y, s.hd.z, s.hd.w, sc, m);
-    const float a = d * static_cast<float>(sc), b = -(dmin * static_cast<float>(m));
-    const uint2 raw = s.qs[KK >> 1];
-    constexpr uint32_t sh = 4 * (KK & 1);
-    const uint32_t lo = nibbles(raw.x >> sh), hi = nibbles(raw.y >> sh);
+    constexpr int e = KK & 1, j = KK >> 1;  // sub-block 2 q + e, its bytes 8 j .. 8 j + 7
+    const uint4 w = s.qs[j >> 1];
+    const uint32_t w0 = (j & 1) ? w.z : w.x, w1 = (j & 1) ? w.w : w.y;
+    constexpr uint32_t sh = 4 * e;
+    const uint32_t lo = nibbles(w0 >> sh), hi = nibbles(w1 >> sh);
     uint4 p;
-    affine4(lo, a, b, p.x, p.y);
-    affine4(hi, a, b, p.z, p.w);
+    affine4(lo, s.a[e], s.b[e], p.x, p.y);
+    affine4(hi, s.a[e], s.b[e], p.z, p.w);
     return __builtin_bit_cast(bf16x8, p);
 }
 
+// Q6_K order: step KK, group q holds values 32 KK + 8 q + i.
 struct Q6KRowState {
     uint2 ql[4];   // ql bytes 64h + 32t2 + 8q .. +7, index 2h + t2
     uint2 qh[2];   // qh bytes 32h + 8q .. +7
@@ -289,6 +313,7 @@ template <>
 struct RowState<WL_TYPE_Q4_K> {
     Q4KRowState s;
     __device__ __forceinline__ void fetch(const uint8_t* blk, int q) { fetch_q4k(blk, q, s); }
+    __device__ __forceinline__ void prepare(int q) { prepare_q4k(s, q); }
     template <int KK>
     __device__ __forceinline__ bf16x8 frag(int) const { return fragment_q4k<KK>(s); }
 };
@@ -296,6 +321,7 @@ template <>
 struct RowState<WL_TYPE_Q6_K> {
     Q6KRowState s;
     __device__ __forceinline__ void fetch(const uint8_t* blk, int q) { fetch_q6k(blk, q, s); }
+    __device__ __forceinline__ void prepare(int) {}
     template <int KK>
     __device__ __forceinline__ bf16x8 frag(int q) const { return fragment_q6k<KK>(s, q); }
 };
@@ -305,24 +331,50 @@ struct RowState<WL_TYPE_Q6_K> {
 // values 8c .. 8c + 7 of token t is slot c ^ (t & 7) of the token's row, so the 8 tokens lr = 0..7 a B-fragment read
 // serves at once sit in 8 different bank groups.
 //
-// B-fragment (token t = 16 n + lr, values 32 KK + 8 q .. + 7) byte address: 512 t + 16 ((4 KK + q) ^ (lr & 7)).
-// With y = q ^ (lr & 7) = 4 y2 + y01 that is 512 lr + 16 y01 + 64 (KK ^ y2) + 8192 n, and 64 (KK ^ y2) =
-// 64 KK + 64 y2 for even KK, 64 KK - 64 y2 for odd KK: two per-lane bases plus a constant offset per (KK, n).
+// B-fragment of token t = 16 n + lr and the 8 values of slot c (values 8 c .. 8 c + 7): byte address
+// 512 t + 16 (c ^ (lr & 7)) = 512 lr + 16 (c ^ (lr & 7)) + 8192 n.
+// Q6_K order, c = 4 KK + q: with y = q ^ (lr & 7) = 4 y2 + y01 that is 512 lr + 16 y01 + 64 (KK ^ y2) + 8192 n, and
+// 64 (KK ^ y2) = 64 KK + 64 y2 for even KK, 64 KK - 64 y2 for odd KK: two per-lane bases plus a constant offset.
+// Q4_K order, c = 8 q + 4 (KK & 1) + (KK >> 1): a per-lane base for each KK (c ^ (lr & 7) = 8 q + (c & 7) ^ (lr & 7)).
+template <int KK>
+constexpr int q4k_slot_low() { return 4 * (KK & 1) + (KK >> 1); }
+
 struct BAddr {
     uint32_t even, odd;
+    uint32_t step[8];
 };
+template <int TYPE>
 __device__ __forceinline__ BAddr b_addr(int lr, int q) {
-    const int y = q ^ (lr & 7), y2 = y >> 2, base = 512 * lr + 16 * (y & 3);
-    return BAddr{static_cast<uint32_t>(base + 64 * y2), static_cast<uint32_t>(base - 64 * y2)};
+    BAddr ba{};
+    const int y = lr & 7;
+    if constexpr (TYPE == WL_TYPE_Q4_K) {
+        const uint32_t base = 512u * lr + 128u * q;
+        ba.step[0] = base + 16u * (q4k_slot_low<0>() ^ y);
+        ba.step[1] = base + 16u * (q4k_slot_low<1>() ^ y);
+        ba.step[2] = base + 16u * (q4k_slot_low<2>() ^ y);
+        ba.step[3] = base + 16u * (q4k_slot_low<3>() ^ y);
+        ba.step[4] = base + 16u * (q4k_slot_low<4>() ^ y);
+        ba.step[5] = base + 16u * (q4k_slot_low<5>() ^ y);
+        ba.step[6] = base + 16u * (q4k_slot_low<6>() ^ y);
+        ba.step[7] = base + 16u * (q4k_slot_low<7>() ^ y);
+    } else {
+        const int yq = q ^ y, y2 = yq >> 2, base = 512 * lr + 16 * (yq & 3);
+        ba.even = static_cast<uint32_t>(base + 64 * y2);
+        ba.odd = static_cast<uint32_t>(base - 64 * y2);
+    }
+    return ba;
 }
-template <int KK>
-__device__ __forceinline__ bf16x8 read_b1(const uint8_t* buf, BAddr ba, int n) {
-    return *reinterpret_cast<const bf16x8*>(buf + ((KK & 1) ? ba.odd : ba.even) + 64 * KK + 8192 * n);
+template <int TYPE, int KK>
+__device__ __forceinline__ bf16x8 read_b1(const uint8_t* buf, const BAddr& ba, int n) {
+    if constexpr (TYPE == WL_TYPE_Q4_K)
+        return *reinterpret_cast<const bf16x8*>(buf + ba.step[KK] + 8192 * n);
+    else
+        return *reinterpret_cast<const bf16x8*>(buf + ((KK & 1) ? ba.odd : ba.even) + 64 * KK + 8192 * n);
 }
-template <int NT, int KK>
-__device__ __forceinline__ void read_b(const uint8_t* buf, BAddr ba, bf16x8 (&b)[8]) {
+template <int TYPE, int NT, int KK>
+__device__ __forceinline__ void read_b(const uint8_t* buf, const BAddr& ba, bf16x8 (&b)[8]) {
 #pragma unroll
-    for (int n = 0; n < NT; n++) b[n] = read_b1<KK>(buf, ba, n);
+    for (int n = 0; n < NT; n++) b[n] = read_b1<TYPE, KK>(buf, ba, n);
 }
 
 // Explicit MFMA / VALU interleave through scheduling barriers (the compiler's default order otherwise). Off: it
@@ -330,31 +382,24 @@ __device__ __forceinline__ void read_b(const uint8_t* buf, BAddr ba, bf16x8 (&b)
 constexpr bool kSchedGroups = false;
 
 // One 32-value step, software-pipelined: the MFMAs of step KK (A-fragments `a`, B-fragments `b`) are interleaved
-// with decoding step KK + 1's A-fragments into `an` (from `nx`, the next block's rows, when KK is the chunk's last
-// step) and, as each b[n] has been consumed, reading step KK + 1's b[n] in its place (the last step's successor
-// reads from the other LDS buffer after the barrier), so the decode runs while the matrix core is busy.
-// The first A-fragments of a block are decoded at the top of its iteration (after the barrier that follows the wait
-// for every outstanding load) rather than in the previous iteration's last step, so the row-state loads have a whole
-// iteration to land instead of seven steps.
-constexpr bool kLateFirst = true;
-
+// with decoding step KK + 1's A-fragments into `an` (the chunk's last step decodes nothing: the next block's first
+// fragments are decoded at the top of the next iteration) and, as each b[n] has been consumed, reading step
+// KK + 1's b[n] in its place (the last step's successor reads from the other LDS buffer after the barrier), so the
+// decode runs while the matrix core is busy.
 template <int TYPE, int NT, int KK>
-__device__ __forceinline__ void gemm_step(const uint8_t* buf, BAddr ba, const RowState<TYPE> (&rs)[kRT],
+__device__ __forceinline__ void gemm_step(const uint8_t* buf, const BAddr& ba, const RowState<TYPE> (&rs)[kRT],
                                           const RowState<TYPE> (&nx)[kRT], floatx4 (&acc)[kRT][8],
                                           const bf16x8 (&a)[kRT], bf16x8 (&b)[8], bf16x8 (&an)[kRT], int q) {
 #pragma unroll
     for (int r = 0; r < kRT; r++) {
-        if constexpr (KK < 7)
-            an[r] = rs[r].template frag<KK + 1>(q);
-        else if constexpr (!kLateFirst)
-            an[r] = nx[r].template frag<0>(q);
+        if constexpr (KK < 7) an[r] = rs[r].template frag<KK + 1>(q);
     }
 #pragma unroll
     for (int n = 0; n < NT; n++) {
 #pragma unroll
         for (int r = 0; r < kRT; r++)
             acc[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r], b[n], acc[r][n], 0, 0, 0);
-        if constexpr (KK < 7) b[n] = read_b1<KK + 1>(buf, ba, n);
+        if constexpr (KK < 7) b[n] = read_b1<TYPE, KK + 1>(buf, ba, n);
     }
     if constexpr (kSchedGroups) {
         // kRT NT MFMAs per step against ~34 kRT VALU instructions of decode
@@ -434,16 +479,12 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
     const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
     const uint32_t lds0 = lds_address(bufs[0]), lds1 = lds_address(bufs[1]);
-    const BAddr ba = b_addr(lr, q);
+    const BAddr ba = b_addr<TYPE>(lr, q);
     RowState<TYPE> rs[kRT], nx[kRT];
 #pragma unroll
     for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr), q);
     stage_async(lds0, src, rowtab, col, wv, half);
     bf16x8 a0[kRT], a1[kRT], b[8];
-    if constexpr (!kLateFirst) {
-#pragma unroll
-        for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
-    }
     for (int kc = 0; kc < nblocks; kc++) {
         wait_stage();     // this chunk's LDS tile has landed
         __syncthreads();  // ... for every wavefront, and the other buffer is free
@@ -453,10 +494,13 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
         if (kc + 1 < nblocks) stage_async((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
                                           rowtab, col, wv, half);
         const uint8_t* buf = bufs[kc & 1];
-        read_b<NT, 0>(buf, ba, b);
-        if constexpr (kLateFirst) {
+        read_b<TYPE, NT, 0>(buf, ba, b);
+        // the block's first fragments are decoded here, after the wait for every outstanding load, rather than in
+        // the previous iteration's last step: the row-state loads get a whole iteration to land
 #pragma unroll
-            for (int r = 0; r < kRT; r++) a0[r] = rs[r].template frag<0>(q);
+        for (int r = 0; r < kRT; r++) {
+            rs[r].prepare(q);
+            a0[r] = rs[r].template frag<0>(q);
         }
         gemm_step<TYPE, NT, 0>(buf, ba, rs, nx, acc, a0, b, a1, q);
         gemm_step<TYPE, NT, 1>(buf, ba, rs, nx, acc, a1, b, a0, q);
