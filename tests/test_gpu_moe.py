@@ -39,18 +39,41 @@ def check_layer(hip, layer, lw, x, label):
     return err
 
 
-@pytest.mark.parametrize("T", [1, 2, 9, 64, 300, 1000])
+@pytest.mark.parametrize("T", [1, 2, 9, 64, 300, 1000, 2100])
 def test_route_c2(hip, c2, layer_c2, T):
-    """Routing bits at token counts that take each router kernel (one token, the per-row GEMV over token
-    groups, the tiled kernel)."""
+    """Routing bits at token counts that take each router kernel (one token, the small-batch kernel, the
+    matrix-core kernel from 2048 tokens): logits bit-exact with the CPU replay of the fixed FMA order."""
     x = synth.tokens(2, T)
-    wts, ids, sg = c2.route(torch.from_numpy(x).cuda())
+    wts, ids, sg, lg = c2.route(torch.from_numpy(x).cuda(), return_logits=True)
     logits = cref.router_logits(x, layer_c2["router"])
+    np.testing.assert_array_equal(lg.cpu().numpy().view(np.uint32), logits.view(np.uint32))
     w_ref, ids_ref = moe_ref.route(logits, 8, True)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_allclose(wts.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
     z = cref.router_logits(x, layer_c2["shared_gate"][None])[:, 0]
     np.testing.assert_allclose(sg.cpu().numpy(), moe_ref.sigmoid(z), rtol=1e-6)
+
+
+@pytest.mark.parametrize("experts,shared_gate,T", [(40, True, 2085), (64, False, 2050), (72, True, 2049)])
+def test_route_variants(hip, experts, shared_gate, T):
+    """The matrix-core router on ragged shapes: expert counts that are not a multiple of its 64-row tiles (the
+    shared gate then rides in the last tile), token counts that are not a multiple of its token tiles, a bias."""
+    lw = synth.moe_layer(80, hidden=1024, inter=256, shared_inter=256, experts=experts, top_k=4, zipf_alpha=1.1)
+    if not shared_gate:
+        lw["shared_gate"] = None
+    layer = hip.MoELayer.from_host(lw)
+    x = synth.tokens(81, T, 1024)
+    wts, ids, sg, lg = layer.route(torch.from_numpy(x).cuda(), return_logits=True)
+    logits = cref.router_logits(x, lw["router"], lw["router_bias"])
+    np.testing.assert_array_equal(lg.cpu().numpy().view(np.uint32), logits.view(np.uint32))
+    w_ref, ids_ref = moe_ref.route(logits, 4, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(wts.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+    if shared_gate:
+        z = cref.router_logits(x, lw["shared_gate"][None])[:, 0]
+        np.testing.assert_allclose(sg.cpu().numpy(), moe_ref.sigmoid(z), rtol=1e-6)
+    else:
+        assert sg is None
 
 
 def test_layer_c2_decode_b1(hip, c2, layer_c2):

@@ -6,7 +6,7 @@
 // registers (fp32 value, rounded to bf16 like Tensor.to(torch.bfloat16)), while the tokens' activations (bf16) are
 // staged in LDS as the B-operand. Accumulation is fp32.
 //
-//   k_router_tiled   logits for many tokens in the router's fixed order (64-value FMA segments, added left to right)
+//   k_router_mfma    logits for many tokens in the router's fixed order (64-value FMA segments, added left to right)
 //   k_to_bf16        x -> bf16
 //   k_tiles          per-expert tiles of up to 128 tokens (sorted positions), then the shared expert's
 //   k_gemm_gate_up   per (tile, 128 intermediate rows): gate and up rows together, epilogue h = silu(g) * u -> bf16
@@ -54,97 +54,126 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Router for many tokens. A workgroup computes a 64-token x 64-row tile (rows: experts, then the shared gate as row
-// E); thread (tx, ty) the 16 outputs of tokens ty + 16 i and rows tx + 16 j (i, j < 4). Per 64-value segment the
-// operands are staged in LDS row-major (64 values + 4 of padding per token or row, so the 16 rows a wavefront reads
-// at once fall in different bank groups), and every output chains 64 fused multiply-adds in ascending k; the
-// segment partial is then added to the running total: the order of router_row and of the CPU replay.
-constexpr int kRtStride = kRouterSeg + 4;
+// Router for many tokens on the matrix core. v_mfma_f32_16x16x4_f32 computes each output as four fused multiply-adds
+// onto the accumulator in k order (c = fma(a[k], b[k], c), k = 0..3, bit for bit the same), so a chain of 16 of them
+// from a zero accumulator over k = 4 s + j (s = 0..15, j = 0..3) is a 64-value segment's fused multiply-add chain in
+// ascending k; each segment partial is then added to the running total: the order of router_row and of the CPU
+// replay. A workgroup computes 32 TM tokens x 64 rows (rows: experts, then the shared gate as row E); wavefront w
+// the TM x 2 tiles of 16 x 16 at tokens 16 TM (w & 1) + 16 m and rows 32 (w >> 1) + 16 n. Per segment the operands
+// are staged in LDS as [j][token or row][s] with 20-float rows: lane (l % 16, j = l / 16) reads its 16 values of the
+// segment as four 16-byte loads, and the 8 lanes of one LDS cycle fall in 8 different bank groups. Segment s + 1 is
+// loaded into registers while segment s is computed.
+constexpr int kRmRow = 20;
+constexpr int kRouterMfmaTM = 1;  // token tiles of 16 per wavefront
 
-__global__ __launch_bounds__(256) void k_router_tiled(const float* __restrict__ x, const float* __restrict__ w,
-                                                      const float* __restrict__ bias,
-                                                      const float* __restrict__ shared_gate, int T, int H, int E,
-                                                      float* __restrict__ logits, float* __restrict__ sg) {
-    __shared__ __attribute__((aligned(16))) float xs[64 * kRtStride];
-    __shared__ __attribute__((aligned(16))) float ws[64 * kRtStride];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int t0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+template <int TM>
+__global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ bias,
+                                                     const float* __restrict__ shared_gate, int T, int H, int E,
+                                                     float* __restrict__ logits, float* __restrict__ sg) {
+    constexpr int kTok = 32 * TM;              // tokens per workgroup
+    constexpr int kXq = kTok * 16 / 256;       // float4 loads per thread per segment (tokens)
+    __shared__ __attribute__((aligned(16))) float xs[4 * kTok * kRmRow];
+    __shared__ __attribute__((aligned(16))) float ws[4 * 64 * kRmRow];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int t0 = blockIdx.x * kTok, r0 = blockIdx.y * 64;
     const int rows = E + (shared_gate ? 1 : 0);
-    float seg[4][4], tot[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) tot[i][j] = 0.0f;
     const int nseg = H / kRouterSeg;
-    // staging: 16 threads per token / row, one float4 each (coalesced loads, conflict-free stores); segment s + 1
-    // is loaded into registers while segment s is computed
-    const int c4 = (tid & 15) * 4;
-    const float* xrow[4];
+    // staging: float4 f = tid + 256 q holds values 4 s4 .. 4 s4 + 3 (s4 = f % 16) of token / row f / 16
+    const int s4 = tid & 15;
+    const float* xrow[kXq];
     const float* wrow[4];
 #pragma unroll
+    for (int q = 0; q < kXq; q++) {
+        const int t = t0 + ((tid + 256 * q) >> 4);
+        xrow[q] = x + static_cast<int64_t>(t < T ? t : T - 1) * H + 4 * s4;
+    }
+#pragma unroll
     for (int q = 0; q < 4; q++) {
-        const int rr = (tid >> 4) + 16 * q, t = t0 + rr, r = r0 + rr;
-        xrow[q] = t < T ? x + static_cast<int64_t>(t) * H + c4 : nullptr;
-        wrow[q] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + c4 : nullptr;
+        const int r = r0 + ((tid + 256 * q) >> 4);
+        wrow[q] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + 4 * s4 : nullptr;
     }
-    float4 xn[4], wn[4];
-    auto load_seg = [&](int s) {
+    float4 xn[kXq], wn[4];
+    auto load_seg = [&](int sgi) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            xn[q] = xrow[q] ? *reinterpret_cast<const float4*>(xrow[q] + s * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
-            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + s * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int q = 0; q < kXq; q++) xn[q] = *reinterpret_cast<const float4*>(xrow[q] + sgi * kRouterSeg);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + sgi * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
+    const int lt = lane & 15, lj = lane >> 4;
+    const int tm0 = 16 * TM * (wv & 1), rn0 = 32 * (wv >> 1);
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    floatx4 tot[TM][2], acc[TM][2];
     load_seg(0);
-    for (int s = 0; s < nseg; s++) {
+    for (int sgi = 0; sgi < nseg; sgi++) {
         __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kXq; q++) {
+            const int rr = (tid + 256 * q) >> 4;
+            xs[(0 * kTok + rr) * kRmRow + s4] = xn[q].x;
+            xs[(1 * kTok + rr) * kRmRow + s4] = xn[q].y;
+            xs[(2 * kTok + rr) * kRmRow + s4] = xn[q].z;
+            xs[(3 * kTok + rr) * kRmRow + s4] = xn[q].w;
+        }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int rr = (tid >> 4) + 16 * q;
-            *reinterpret_cast<float4*>(&xs[rr * kRtStride + c4]) = xn[q];
-            *reinterpret_cast<float4*>(&ws[rr * kRtStride + c4]) = wn[q];
+            const int rr = (tid + 256 * q) >> 4;
+            ws[(0 * 64 + rr) * kRmRow + s4] = wn[q].x;
+            ws[(1 * 64 + rr) * kRmRow + s4] = wn[q].y;
+            ws[(2 * 64 + rr) * kRmRow + s4] = wn[q].z;
+            ws[(3 * 64 + rr) * kRmRow + s4] = wn[q].w;
         }
         __syncthreads();
-        if (s + 1 < nseg) load_seg(s + 1);
+        if (sgi + 1 < nseg) load_seg(sgi + 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
+            float4 av[TM], bv[2];
 #pragma unroll
-            for (int j = 0; j < 4; j++) seg[i][j] = 0.0f;
-#pragma unroll 4
-        for (int kk = 0; kk < kRouterSeg; kk += 4) {
-            float4 xv[4], wv[4];
+            for (int m = 0; m < TM; m++)
+                av[m] = *reinterpret_cast<const float4*>(&xs[(lj * kTok + tm0 + 16 * m + lt) * kRmRow + 4 * q]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const float4*>(&xs[(ty + 16 * i) * kRtStride + kk]);
+            for (int n = 0; n < 2; n++)
+                bv[n] = *reinterpret_cast<const float4*>(&ws[(lj * 64 + rn0 + 16 * n + lt) * kRmRow + 4 * q]);
 #pragma unroll
-            for (int j = 0; j < 4; j++) wv[j] = *reinterpret_cast<const float4*>(&ws[(tx + 16 * j) * kRtStride + kk]);
+            for (int u = 0; u < 4; u++) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int m = 0; m < TM; m++) {
+                    const float a = u == 0 ? av[m].x : u == 1 ? av[m].y : u == 2 ? av[m].z : av[m].w;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    seg[i][j] = __builtin_fmaf(xv[i].x, wv[j].x, seg[i][j]);
-                    seg[i][j] = __builtin_fmaf(xv[i].y, wv[j].y, seg[i][j]);
-                    seg[i][j] = __builtin_fmaf(xv[i].z, wv[j].z, seg[i][j]);
-                    seg[i][j] = __builtin_fmaf(xv[i].w, wv[j].w, seg[i][j]);
+                    for (int n = 0; n < 2; n++) {
+                        const float b = u == 0 ? bv[n].x : u == 1 ? bv[n].y : u == 2 ? bv[n].z : bv[n].w;
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, (q == 0 && u == 0) ? zero : acc[m][n],
+                                                                         0, 0, 0);
+                    }
                 }
+            }
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int m = 0; m < TM; m++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) tot[i][j] = s == 0 ? seg[i][j] : __fadd_rn(tot[i][j], seg[i][j]);
+            for (int n = 0; n < 2; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) tot[m][n][i] = sgi == 0 ? acc[m][n][i] : __fadd_rn(tot[m][n][i], acc[m][n][i]);
     }
+    // lane holds D[4 lj + i][lt]: token tm0 + 16 m + 4 lj + i, row rn0 + 16 n + lt
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = t0 + ty + 16 * i;
-        if (t >= T) continue;
+    for (int m = 0; m < TM; m++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r = r0 + tx + 16 * j;
-            if (r < E)
-                logits[static_cast<int64_t>(t) * E + r] = bias ? __fadd_rn(tot[i][j], bias[r]) : tot[i][j];
-            else if (r == E && shared_gate)
-                sg[t] = sigmoid(tot[i][j]);
+        for (int n = 0; n < 2; n++) {
+            const int r = r0 + rn0 + 16 * n + lt;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + tm0 + 16 * m + 4 * lj + i;
+                if (t < T && r < rows) {
+                    const float v = tot[m][n][i];
+                    if (r < E)
+                        logits[static_cast<int64_t>(t) * E + r] = bias ? __fadd_rn(v, bias[r]) : v;
+                    else
+                        sg[t] = sigmoid(v);
+                }
+            }
         }
-    }
 }
 
 // x fp32 -> bf16, 8 values per thread.
@@ -650,9 +679,11 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
     const bool separate = shared_gate && L.n_experts % 64 == 0;
     const float* tiled_gate = separate ? nullptr : shared_gate;
     const int rows = L.n_experts + (tiled_gate ? 1 : 0);
-    const dim3 grid(static_cast<unsigned>((T + 63) / 64), static_cast<unsigned>((rows + 63) / 64));
-    k_router_tiled<<<grid, 256, 0, s>>>(x, L.router, L.router_bias, tiled_gate, static_cast<int>(T), L.hidden,
-                                        L.n_experts, logits, sg);
+    const unsigned rtiles = static_cast<unsigned>((rows + 63) / 64);
+    k_router_mfma<kRouterMfmaTM><<<dim3(static_cast<unsigned>((T + 32 * kRouterMfmaTM - 1) / (32 * kRouterMfmaTM)),
+                                        rtiles),
+                                   256, 0, s>>>(x, L.router, L.router_bias, tiled_gate, static_cast<int>(T), L.hidden,
+                                                L.n_experts, logits, sg);
     if (separate)
         k_router_sg<<<static_cast<unsigned>((T + 7) / 8), 256, 0, s>>>(x, shared_gate, static_cast<int>(T),
                                                                        L.hidden, sg);

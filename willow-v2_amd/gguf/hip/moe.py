@@ -110,9 +110,10 @@ class MoELayer:
                                      _ptr(weights), ws.data_ptr(), ws.numel(), _stream(self.device)))
         return y
 
-    def route(self, x: torch.Tensor):
+    def route(self, x: torch.Tensor, return_logits: bool = False):
         """-> (weights fp32 [T, top_k], ids int32 [T, top_k], shared gate fp32 [T] or None): engines/base.py:91-97
-        on the router logits, plus sigmoid(x . shared_gate)."""
+        on the router logits, plus sigmoid(x . shared_gate); with return_logits also the logits fp32 [T, E]
+        (bias included)."""
         xf = x.reshape(-1, self.hidden).to(torch.float32).contiguous()
         tokens = xf.shape[0]
         logits = torch.empty(tokens, self.n_experts, dtype=torch.float32, device=self.device)
@@ -123,6 +124,8 @@ class MoELayer:
             sg = torch.empty(tokens, dtype=torch.float32, device=self.device)
         check(library().wl_moe_route(ctypes.byref(self.struct), xf.data_ptr(), tokens, logits.data_ptr(),
                                      ids.data_ptr(), weights.data_ptr(), _ptr(sg), _stream(self.device)))
+        if return_logits:
+            return weights, ids, sg, logits
         return weights, ids, sg
 
 
