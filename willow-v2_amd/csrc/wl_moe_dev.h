@@ -110,11 +110,26 @@ __device__ __forceinline__ float softmax_sum(const float* __restrict__ lt, int E
 __device__ __forceinline__ float pick_weight(float my_v, float m, float s, int k, bool renorm, int lane) {
     const float p = lane < k ? expf(my_v - m) / s : 0.0f;
     float wsum = 0.0f;
-    for (int r = 0; r < k; r++) {
-        const float pr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), r));
-        wsum = r == 0 ? pr : wsum + pr;
+    // 8 picks' readlanes at a time (independent), added in pick order
+    for (int r0 = 0; r0 < k; r0 += 8) {
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            pr[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), (r0 + i) & 63));
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (r0 + i < k) wsum = r0 + i == 0 ? pr[i] : wsum + pr[i];
     }
     return renorm ? p / wsum : p;
+}
+
+// max(v, the value of the lane DPP control CTRL selects) on unsigned 32-bit values, every lane sourcing
+__device__ __forceinline__ int umax_dpp_impl(int v, int o) {
+    return static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(o)));
+}
+template <int CTRL>
+__device__ __forceinline__ int umax_dpp(int v) {
+    return umax_dpp_impl(v, __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false));
 }
 
 template <int EJ>

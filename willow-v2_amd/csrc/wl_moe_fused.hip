@@ -108,10 +108,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_wsel[kFusedMaxK];
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
-    __shared__ uint64_t lds_key[kFusedMaxE];
-    __shared__ uint64_t lds_cand[kFusedMaxE];
-    __shared__ uint64_t lds_gmax[kFusedMaxE / 32];
-    __shared__ int lds_wcount[kFusedWaves];
+    __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int b = blockIdx.x, G = a.G;
@@ -195,63 +192,106 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
              [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
              [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
          ok;
-    // top-k by rank among candidates. Key: the order key and the inverted id (larger first, ties to the lower
-    // id; 64 bits, all distinct). T0 = the smallest of the 8 half-wavefront maxima over keys 0..255: at least 8
-    // distinct keys are >= T0, so the top k (k <= 8) are among the candidates key >= T0 (typically 8 to 20, all
-    // 256 at worst); each candidate counts the candidates above it, and the k of rank < k place themselves.
-    // Wavefront 0 then computes the weights as wave_topk does.
-    {
-        const int i = threadIdx.x;
-        uint64_t key = 0;  // below every logit's
-        if (i < kFusedMaxE) {
-            if (i < E) {
-                const float v = lds_logits[i];
-                key = (static_cast<uint64_t>(order_key(v == v ? v : -INFINITY)) << 32) | (0xFFFFFFFFu - i);
-            }
-            lds_key[i] = key;
-        }
-        __syncthreads();
-        if (i < kFusedMaxE / 32) {  // 8 threads: the maximum of keys 32 i .. 32 i + 31
-            uint64_t mx = 0;
-            for (int u = 0; u < 32; u++) mx = lds_key[32 * i + u] > mx ? lds_key[32 * i + u] : mx;
-            lds_gmax[i] = mx;
-        }
-        __syncthreads();
-        uint64_t t0 = lds_gmax[0];
-#pragma unroll
-        for (int g = 1; g < kFusedMaxE / 32; g++) t0 = lds_gmax[g] < t0 ? lds_gmax[g] : t0;
-        const bool cand = i < E && key >= t0;
-        // compaction: the candidates' keys in index order
-        const uint64_t wm = __ballot(cand);
-        if (lane == 0) lds_wcount[wv] = __popcll(wm);
-        __syncthreads();
-        int base = 0, n_cand = 0;
-#pragma unroll
-        for (int w = 0; w < kFusedWaves; w++) {
-            base += w < wv ? lds_wcount[w] : 0;
-            n_cand += lds_wcount[w];
-        }
-        if (cand) lds_cand[base + __popcll(wm & __lanemask_lt())] = key;
-        __syncthreads();
-        if (cand) {
-            int above = 0;
-            for (int u = 0; u < n_cand; u++) above += lds_cand[u] > key ? 1 : 0;
-            if (above < k) lds_pick[above] = i;
-        }
-        __syncthreads();
-    }
+    // top-k, in wavefront 0. Lane l holds logits l + 64 j. The 8 groups of 32 logits (j, half of the wavefront)
+    // reduce their order keys to the maximum (DPP within rows of 16, then a row broadcast); with T0 the smallest
+    // maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at least k the
+    // top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The candidates
+    // (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are compacted
+    // in LDS and each counts the candidates above it: up to 32 of them in one fixed pass over a zero-padded list.
+    // The k of rank < k place themselves; the weights follow wave_topk's arithmetic.
+    static_assert(kFusedMaxK <= 8, "");
     if (wv == 0) {
-        // the max logit is pick 0's (softmax_stats' max, bitwise)
-        const float lv0 = lds_logits[lds_pick[0]];
-        const float m = lv0 == lv0 ? lv0 : -INFINITY;
-        const float ssum = softmax_sum<EJ>(lds_logits, E, lane, m);
+        float v[EJ];
+        uint32_t k32[EJ];
+        bool valid[EJ];
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            const int idx = lane + 64 * j;
+            valid[j] = idx < E;
+            const float lv = valid[j] ? lds_logits[idx] : -INFINITY;
+            v[j] = lv == lv ? lv : -INFINITY;
+            k32[j] = valid[j] ? order_key(v[j]) : 0u;  // 0: below every logit's
+        }
+        if (lane < 32) lds_cand[lane] = 0;  // below every candidate's key
+        const int ng = (E + 31) / 32;
+        uint32_t t0 = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            int u = static_cast<int>(k32[j]);
+            u = umax_dpp<0xB1>(u);   // quad_perm [1,0,3,2]
+            u = umax_dpp<0x4E>(u);   // quad_perm [2,3,0,1]
+            u = umax_dpp<0x141>(u);  // row_half_mirror
+            u = umax_dpp<0x140>(u);  // row_mirror: every lane holds its row's maximum
+            // row_bcast:15 into rows 1 and 3: lanes 31 and 63 then hold the maxima of lanes 0..31 and 32..63
+            u = static_cast<int>(max(static_cast<uint32_t>(u),
+                                     static_cast<uint32_t>(__builtin_amdgcn_update_dpp(u, u, 0x142, 0xA, 0xF, false))));
+            if (2 * j < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 31)));
+            if (2 * j + 1 < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 63)));
+        }
+        if (ng < k) t0 = 0;
+        lane_sync();
+        int n_cand = 0;
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            const int idx = lane + 64 * j;
+            const bool cand = valid[j] && k32[j] >= t0;
+            const uint64_t m = __ballot(cand);
+            if (cand)
+                lds_cand[n_cand + __popcll(m & __lanemask_lt())] =
+                    (static_cast<uint64_t>(k32[j]) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(idx));
+            n_cand += __popcll(m);
+        }
+        lane_sync();
+        uint64_t ck[EJ];
+        int above[EJ];
+#pragma unroll
+        for (int q = 0; q < EJ; q++) {
+            const int u = lane + 64 * q;
+            ck[q] = u < n_cand ? lds_cand[u] : 0;
+            above[q] = 0;
+        }
+        if (n_cand <= 32) {
+#pragma unroll
+            for (int u = 0; u < 32; u += 2) {
+                const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u]);
+                const uint64_t o0 = (static_cast<uint64_t>(r.y) << 32) | r.x;
+                const uint64_t o1 = (static_cast<uint64_t>(r.w) << 32) | r.z;
+                above[0] += (o0 > ck[0] ? 1 : 0) + (o1 > ck[0] ? 1 : 0);
+            }
+        } else {
+            for (int u0 = 0; u0 < n_cand; u0 += 2) {  // entries past n_cand (< kFusedMaxE) are never counted
+                const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u0]);
+                const uint64_t o0 = (static_cast<uint64_t>(r.y) << 32) | r.x;
+                const uint64_t o1 = (static_cast<uint64_t>(r.w) << 32) | r.z;
+#pragma unroll
+                for (int q = 0; q < EJ; q++)
+                    above[q] += (o0 > ck[q] ? 1 : 0) + ((u0 + 1 < n_cand && o1 > ck[q]) ? 1 : 0);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < EJ; q++)
+            if (lane + 64 * q < n_cand && above[q] < k)
+                lds_pick[above[q]] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck[q]));
+        lane_sync();
+        // the max logit is pick 0's (softmax_stats' max, bitwise); the sum as softmax_sum adds it
         const int my_id = lane < k ? lds_pick[lane] : 0;
+        const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
+        const float m = lv0 == lv0 ? lv0 : -INFINITY;
+        float ssum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EJ; j++)
+            if (valid[j]) ssum += expf(v[j] - m);
+        ssum = group_sum<64>(ssum);
         const float lv = lds_logits[my_id];
         const float my_w = pick_weight(lane < k ? (lv == lv ? lv : -INFINITY) : -INFINITY, m, ssum, k,
                                        a.renorm != 0, lane);
+        int idr[kFusedMaxK];
+#pragma unroll
+        for (int q = 0; q < kFusedMaxK; q++) idr[q] = __builtin_amdgcn_readlane(my_id, q);
+        int my_rank = 0;  // position among the k ids in ascending order
+#pragma unroll
+        for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && idr[q] < my_id) ? 1 : 0;
         if (lane < k) {
-            int my_rank = 0;  // position among the k ids in ascending order
-            for (int q = 0; q < k; q++) my_rank += lds_pick[q] < my_id ? 1 : 0;
             lds_sel[my_rank] = my_id;
             lds_wsel[my_rank] = my_w;
             if (b == 0) {
