@@ -52,7 +52,8 @@ struct ExpertArgs {
     float* o_sh;
 };
 
-constexpr int kTileTokens = 128;             // prefill: tokens per GEMM tile
+constexpr int kTileTokens = 144;             // prefill: tokens per gate_up GEMM tile (9 MFMA token tiles)
+constexpr int kDownTileTokens = 128;         // prefill: tokens per down GEMM tile (8 MFMA token tiles)
 constexpr int kGemvMaxTokens = 8;  // fp32 GEMV experts up to this many tokens, bf16 MFMA GEMMs above (gguf/metal.py:20)
 constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
 
@@ -65,8 +66,10 @@ struct PrefillArgs {
     const uint8_t* sh_down;
     const uint16_t* xb;      // [T, H] bf16
     const int32_t* sorted;   // [T*k] pair id by sorted position
-    const int4* tiles;       // (expert or E for the shared expert, first position / token, count)
+    const int4* tiles;       // gate_up tiles: (expert or E for the shared expert, first position / token, count)
     const int32_t* n_tiles;
+    const int4* tiles_down;  // down tiles, the same of at most kDownTileTokens tokens
+    const int32_t* n_tiles_down;
     uint16_t* h16;           // [T*k, inter] bf16 by sorted position
     uint16_t* h_sh16;        // [T, shared_inter] bf16
     float* o;                // [T*k, H]
@@ -94,8 +97,9 @@ struct Workspace {
     float* o_sh;        // [T, hidden]
     // prefill (MFMA) path only
     uint16_t* xb;       // [T, hidden] bf16
-    int4* tiles;        // [max_tiles]
-    int32_t* n_tiles;   // [1]
+    int4* tiles;        // [max_tiles(kTileTokens)]
+    int4* tiles_down;   // [max_tiles(kDownTileTokens)]
+    int32_t* n_tiles;   // [2]: gate_up tiles, down tiles
     uint16_t* h16;      // [T*k, inter] bf16
     uint16_t* h_sh16;   // [T, shared_inter] bf16
     size_t bytes;
@@ -108,7 +112,7 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
                  hipStream_t s);
 int zero_sync(void* workspace, hipStream_t s);
 bool prefill_eligible(const WlMoeLayer& L, int64_t T);
-int max_tiles(const WlMoeLayer& L, int64_t T);
+int max_tiles(const WlMoeLayer& L, int64_t T, int cap);
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s);
 int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s);
 

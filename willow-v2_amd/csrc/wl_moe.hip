@@ -531,8 +531,9 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.o_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.hidden : 0));
     const bool mfma = prefill_eligible(L, T);
     w.xb = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * T * L.hidden : 0));
-    w.tiles = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T) : 0));
-    w.n_tiles = static_cast<int32_t*>(take(mfma ? sizeof(int32_t) : 0));
+    w.tiles = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kTileTokens) : 0));
+    w.tiles_down = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kDownTileTokens) : 0));
+    w.n_tiles = static_cast<int32_t*>(take(mfma ? 2 * sizeof(int32_t) : 0));
     w.h16 = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * P * L.inter : 0));
     w.h_sh16 = static_cast<uint16_t*>(take(mfma && shared ? sizeof(uint16_t) * T * L.shared_inter : 0));
     w.bytes = off;

@@ -28,7 +28,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 256;              // k per staged chunk: one K-quant block per row
 constexpr int kTileRowBytes = kBK * 2;                     // one token's chunk in LDS: 512 bytes, 32 slots of 16
-constexpr int kTileBytes = kTileTokens * kTileRowBytes;     // 64 KiB per buffer
+template <int TILE>
+constexpr int tile_bytes() { return TILE * kTileRowBytes; }  // one LDS buffer: 72 KiB for 144 tokens
 // A GEMM workgroup covers 16 row tiles of 16 rows against one token tile: kGemmWaves wavefronts of kRT row tiles
 // each. Two row tiles per wavefront keep a wavefront within 256 registers, so the 8 wavefronts of a workgroup run
 // two per SIMD and one's dequantization overlaps the other's waits.
@@ -185,22 +186,21 @@ __global__ __launch_bounds__(256) void k_to_bf16(const float* __restrict__ x, ui
     reinterpret_cast<uint4*>(xb)[i] = make_uint4(pack2(a.x, a.y), pack2(a.z, a.w), pack2(b.x, b.y), pack2(b.z, b.w));
 }
 
-// Tiles of up to kTileTokens tokens: each routed expert's sorted positions, then the shared expert's tokens
-// (expert id E). tiles[i] = (expert, first position or token, count); n_tiles[0] = how many.
-// One workgroup of 256 threads, thread i owning experts 4i .. 4i + 3 (E <= 1024): tile counts, an exclusive scan
-// of them across the workgroup, then each thread writes its experts' tiles in expert order.
-__global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offsets, int E, int T, int with_shared,
-                                               int4* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
-    __shared__ int scan[2][256];
+// Tiles: each routed expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles of at
+// most `cap` tokens; tiles[i] = (expert, first position or token, count), n_tiles[0] = how many. One workgroup of
+// 256 threads, thread i owning experts 4i .. 4i + 3 (E <= 1024): tile counts, an exclusive scan of them across the
+// workgroup, then each thread writes its experts' tiles in expert order. Two lists, for the two GEMMs' tile sizes.
+__device__ void tile_list(const int32_t* __restrict__ offsets, int E, int T, int with_shared, int cap,
+                          int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int (&scan)[2][256]) {
     const int tid = threadIdx.x;
-    int cnt[4], mine = 0;
+    int mine = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = 4 * tid + i;
-        cnt[i] = e < E ? (offsets[e + 1] - offsets[e] + kTileTokens - 1) / kTileTokens : 0;
-        mine += cnt[i];
+        mine += e < E ? (offsets[e + 1] - offsets[e] + cap - 1) / cap : 0;
     }
     int cur = 0;
+    __syncthreads();  // scan is free (a previous list's reads are done)
     scan[0][tid] = mine;
     __syncthreads();
     for (int off = 1; off < 256; off <<= 1) {
@@ -216,14 +216,21 @@ __global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offse
         const int e = 4 * tid + i;
         if (e >= E) break;
         const int b = offsets[e], c = offsets[e + 1] - b;
-        for (int p = 0; p < c; p += kTileTokens) tiles[n++] = make_int4(e, b + p, min(kTileTokens, c - p), 0);
+        for (int p = 0; p < c; p += cap) tiles[n++] = make_int4(e, b + p, min(cap, c - p), 0);
     }
     int m = total;
     if (with_shared)
-        for (int p = tid * kTileTokens; p < T; p += 256 * kTileTokens)
-            tiles[total + p / kTileTokens] = make_int4(E, p, min(kTileTokens, T - p), 0);
-    if (with_shared) m += (T + kTileTokens - 1) / kTileTokens;
+        for (int p = tid * cap; p < T; p += 256 * cap) tiles[total + p / cap] = make_int4(E, p, min(cap, T - p), 0);
+    if (with_shared) m += (T + cap - 1) / cap;
     if (tid == 0) n_tiles[0] = m;
+}
+
+__global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offsets, int E, int T, int with_shared,
+                                               int4* __restrict__ tiles, int4* __restrict__ tiles_down,
+                                               int32_t* __restrict__ n_tiles) {
+    __shared__ int scan[2][256];
+    tile_list(offsets, E, T, with_shared, kTileTokens, tiles, n_tiles, scan);
+    tile_list(offsets, E, T, with_shared, kDownTileTokens, tiles_down, n_tiles + 1, scan);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -401,7 +408,7 @@ __device__ __forceinline__ bf16x8 read_b1(const uint8_t* buf, const BAddr& ba, i
         return *reinterpret_cast<const bf16x8*>(buf + ((KK & 1) ? ba.odd : ba.even) + 64 * KK + 8192 * n);
 }
 template <int TYPE, int NT, int KK>
-__device__ __forceinline__ void read_b(const uint8_t* buf, const BAddr& ba, bf16x8 (&b)[8]) {
+__device__ __forceinline__ void read_b(const uint8_t* buf, const BAddr& ba, bf16x8 (&b)[NT]) {
 #pragma unroll
     for (int n = 0; n < NT; n++) b[n] = read_b1<TYPE, KK>(buf, ba, n);
 }
@@ -415,10 +422,10 @@ constexpr bool kSchedGroups = false;
 // fragments are decoded at the top of the next iteration) and, as each b[n] has been consumed, reading step
 // KK + 1's b[n] in its place (the last step's successor reads from the other LDS buffer after the barrier), so the
 // decode runs while the matrix core is busy.
-template <int TYPE, int NT, int KK>
+template <int TYPE, int NT, int KK, int NTA>
 __device__ __forceinline__ void gemm_step(const uint8_t* buf, const BAddr& ba, const RowState<TYPE> (&rs)[kRT],
-                                          const RowState<TYPE> (&nx)[kRT], floatx4 (&acc)[kRT][8],
-                                          const bf16x8 (&a)[kRT], bf16x8 (&b)[8], bf16x8 (&an)[kRT], int q) {
+                                          floatx4 (&acc)[kRT][NTA], const bf16x8 (&a)[kRT], bf16x8 (&b)[NT],
+                                          bf16x8 (&an)[kRT], int q) {
 #pragma unroll
     for (int r = 0; r < kRT; r++) {
         if constexpr (KK < 7) an[r] = rs[r].template frag<KK + 1>(q);
@@ -447,35 +454,34 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, const BAddr& ba, c
 // wavefront w fills rows 2 W it + 2 w + (lane >> 5); lane slot s = lane & 31 of row t takes the 16 bytes of values
 // 8 (s ^ (t & 7)) .. + 7, and t & 7 = (2 w + (lane >> 5)) & 7 does not depend on it (2 W is a multiple of 8), so
 // the lane's byte column `col` is fixed. The rows' byte offsets come from `rowtab`, laid out so that a lane's
-// kStageIters are contiguous: rowtab[kStageIters (t % 2 W) + t / 2 W].
+// stage_iters (TILE / 16) are contiguous: rowtab[stage_iters (t % 2 W) + t / 2 W].
 //
 // The loads are issued from inline assembly so that the compiler, which cannot tell the two LDS buffers apart,
 // does not wait for them before the next LDS read of the other buffer; the K loop waits for them itself
 // (s_waitcnt vmcnt(0) and a barrier) before the buffer is read.
-constexpr int kStageIters = kTileBytes / (kGemmWaves * 1024);  // 8
-static_assert(kGemmWaves % 4 == 0 && kStageIters % 4 == 0 && kTileTokens == 2 * kGemmWaves * kStageIters, "");
+template <int TILE>
+constexpr int stage_iters() { return tile_bytes<TILE>() / (kGemmWaves * 1024); }  // 9 for 144 tokens
+static_assert(kGemmWaves % 4 == 0 && kTileTokens % (2 * kGemmWaves) == 0 && kDownTileTokens % (2 * kGemmWaves) == 0,
+              "");
+template <int TILE>
 __host__ __device__ constexpr int rowtab_index(int t) {
-    return kStageIters * (t % (2 * kGemmWaves)) + t / (2 * kGemmWaves);
+    return stage_iters<TILE>() * (t % (2 * kGemmWaves)) + t / (2 * kGemmWaves);
 }
 
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
 }
 
+template <int TILE>
 __device__ __forceinline__ void stage_async(uint32_t buf, const uint8_t* src, const uint32_t* rowtab, uint32_t col,
                                             int wv, int half) {
-    const uint4* tab = reinterpret_cast<const uint4*>(rowtab + kStageIters * (2 * wv + half));
-    uint32_t off[kStageIters];
+    constexpr int kIters = stage_iters<TILE>();
+    const uint32_t* tab = rowtab + kIters * (2 * wv + half);
+    uint32_t off[kIters];
 #pragma unroll
-    for (int i = 0; i < kStageIters / 4; i++) {
-        const uint4 v = tab[i];
-        off[4 * i] = v.x;
-        off[4 * i + 1] = v.y;
-        off[4 * i + 2] = v.z;
-        off[4 * i + 3] = v.w;
-    }
+    for (int i = 0; i < kIters; i++) off[i] = tab[i];
 #pragma unroll
-    for (int it = 0; it < kStageIters; it++) {
+    for (int it = 0; it < kIters; it++) {
         // M0 (the LDS destination) is a register the compiler reserves: saved and restored around the load
         uint32_t saved;
         asm volatile(
@@ -501,8 +507,8 @@ __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 // The K loop for NT token tiles. Block kc + 1's row states and LDS tile are requested at the top of iteration kc;
 // the last iteration requests the row states of its own block again (keeping the loop free of branches around the
 // register loads) and no tile.
-template <int TYPE, int NT, typename RowPtr>
-__device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[kRT][8], int nblocks,
+template <int TYPE, int TILE, int NT, int NTA, typename RowPtr>
+__device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][NTA], int nblocks,
                                           const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr, int lr, int q) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
@@ -512,15 +518,15 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
     RowState<TYPE> rs[kRT], nx[kRT];
 #pragma unroll
     for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr), q);
-    stage_async(lds0, src, rowtab, col, wv, half);
-    bf16x8 a0[kRT], a1[kRT], b[8];
+    stage_async<TILE>(lds0, src, rowtab, col, wv, half);
+    bf16x8 a0[kRT], a1[kRT], b[NT];
     for (int kc = 0; kc < nblocks; kc++) {
         wait_stage();     // this chunk's LDS tile has landed
         __syncthreads();  // ... for every wavefront, and the other buffer is free
         const int kn = kc + 1 < nblocks ? kc + 1 : kc;
 #pragma unroll
         for (int r = 0; r < kRT; r++) nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
-        if (kc + 1 < nblocks) stage_async((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
+        if (kc + 1 < nblocks) stage_async<TILE>((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
                                           rowtab, col, wv, half);
         const uint8_t* buf = bufs[kc & 1];
         read_b<TYPE, NT, 0>(buf, ba, b);
@@ -531,14 +537,14 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
             rs[r].prepare(q);
             a0[r] = rs[r].template frag<0>(q);
         }
-        gemm_step<TYPE, NT, 0>(buf, ba, rs, nx, acc, a0, b, a1, q);
-        gemm_step<TYPE, NT, 1>(buf, ba, rs, nx, acc, a1, b, a0, q);
-        gemm_step<TYPE, NT, 2>(buf, ba, rs, nx, acc, a0, b, a1, q);
-        gemm_step<TYPE, NT, 3>(buf, ba, rs, nx, acc, a1, b, a0, q);
-        gemm_step<TYPE, NT, 4>(buf, ba, rs, nx, acc, a0, b, a1, q);
-        gemm_step<TYPE, NT, 5>(buf, ba, rs, nx, acc, a1, b, a0, q);
-        gemm_step<TYPE, NT, 6>(buf, ba, rs, nx, acc, a0, b, a1, q);
-        gemm_step<TYPE, NT, 7>(buf, ba, rs, nx, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 0, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 1, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 2, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 3, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 4, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 5, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 6, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 7, NTA>(buf, ba, rs, acc, a1, b, a0, q);
 #pragma unroll
         for (int r = 0; r < kRT; r++) rs[r] = nx[r];
     }
@@ -547,28 +553,32 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][kTileBytes], floatx
 
 // ---------------------------------------------------------------------------------------------------------------
 // The GEMM core: a workgroup of kGemmWaves wavefronts, each owning kRT row tiles of 16 (rows given by
-// row_ptr(r, lr)) and the tile's (up to) 128 tokens as 8 token tiles (4 when the tile has at most 64 tokens). Per K
-// chunk of 256 values (one block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value
-// steps decodes kRT A-fragments and runs kRT x NT MFMAs. src_row(t) is token t's row in src ([*, ld] bf16); rows past count load token 0's (their
-// results are never stored).
-template <int TYPE, typename RowPtr, typename SrcRow>
-__device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][kTileBytes], floatx4 (&acc)[kRT][8], int nblocks,
+// row_ptr(r, lr)) and the tile's up to TILE tokens as NT token tiles of 16 (NT = TILE / 16, 8 or 4, the fewest
+// that cover `count`). Per K chunk of 256 values (one block per row) the activations sit in LDS, double-buffered, and each
+// of the 8 32-value steps decodes kRT A-fragments and runs kRT x NT MFMAs. src_row(t) is token t's row in src
+// ([*, ld] bf16); rows past count load token 0's (their results are never stored).
+template <int TYPE, int TILE, typename RowPtr, typename SrcRow>
+__device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][TILE / 16],
+                                          int nblocks,
                                           int count, const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
                                           RowPtr row_ptr) {
-    __shared__ __attribute__((aligned(16))) uint32_t rowtab[kTileTokens];
+    constexpr int NTA = TILE / 16;
+    __shared__ __attribute__((aligned(16))) uint32_t rowtab[TILE];
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
-    for (int t = threadIdx.x; t < kTileTokens; t += blockDim.x)
-        rowtab[rowtab_index(t)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
+    for (int t = threadIdx.x; t < TILE; t += blockDim.x)
+        rowtab[rowtab_index<TILE>(t)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
 #pragma unroll
     for (int r = 0; r < kRT; r++)
 #pragma unroll
-        for (int n = 0; n < 8; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NTA; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();
     const uint8_t* s8 = uniform_ptr(reinterpret_cast<const uint8_t*>(src));
-    if (count > 64)
-        gemm_loop<TYPE, 8>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+    if (NTA > 8 && count > 128)
+        gemm_loop<TYPE, TILE, NTA, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+    else if (count > 64)
+        gemm_loop<TYPE, TILE, 8, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
     else
-        gemm_loop<TYPE, 4>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+        gemm_loop<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its own L2. slab_tile maps the linear
@@ -586,7 +596,7 @@ __device__ __forceinline__ void slab_tile(int nslab, int& slab, int& tile) {
 // and the matching up rows inter + j0 + ... (r >= kRT / 2), j0 = 128 slab + 8 kRT w. Epilogue h = silu(g) * u -> bf16.
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kTileTokens>()];
     int slab, ti;
     slab_tile(a.nslab_gate_up, slab, ti);
     if (ti >= a.n_tiles[0]) return;
@@ -600,19 +610,19 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
-    floatx4 acc[kRT][8];
+    floatx4 acc[kRT][kTileTokens / 16];
     auto row_ptr = [&](int r, int lr) {
         const int j = j0 + 16 * (r % kHalf) + lr;
         return W + static_cast<int64_t>((r < kHalf ? 0 : inter) + j) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
-    gemm_tile<TYPE>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
+    gemm_tile<TYPE, kTileTokens>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     uint16_t* out = sh ? a.h_sh16 : a.h16;
 #pragma unroll
     for (int r = 0; r < kHalf; r++) {
 #pragma unroll
-        for (int n = 0; n < 8; n++) {
+        for (int n = 0; n < kTileTokens / 16; n++) {
             const int t = 16 * n + lr;
             if (t < count) {
                 const int j = j0 + 16 * r + 4 * q;
@@ -626,13 +636,14 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
 }
 
 // down: slab = 256-row slab of the hidden dim; wavefront w: rows r0 + 16 kRT w + 16 r + lr. o fp32 by position.
+// Its tiles hold at most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts within 256 registers).
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kDownTileTokens>()];
     int slab, ti;
     slab_tile(a.H / 256, slab, ti);
-    if (ti >= a.n_tiles[0]) return;
-    const int4 tile = a.tiles[ti];
+    if (ti >= a.n_tiles_down[0]) return;
+    const int4 tile = a.tiles_down[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
     const int row0 = slab * 256 + 16 * kRT * (threadIdx.x >> 6);
@@ -640,16 +651,16 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     const int nb = inter / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
-    floatx4 acc[kRT][8];
+    floatx4 acc[kRT][kDownTileTokens / 16];
     auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>(row0 + 16 * r + lr) * rs; };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
-    gemm_tile<TYPE>(bufs, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
+    gemm_tile<TYPE, kDownTileTokens>(bufs, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     float* out = sh ? a.o_sh : a.o;
 #pragma unroll
     for (int r = 0; r < kRT; r++) {
 #pragma unroll
-        for (int n = 0; n < 8; n++) {
+        for (int n = 0; n < kDownTileTokens / 16; n++) {
             const int t = 16 * n + lr;
             if (t < count) {
                 const floatx4 v = acc[r][n];
@@ -690,10 +701,10 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
     return launch_status();
 }
 
-int max_tiles(const WlMoeLayer& L, int64_t T) {
+int max_tiles(const WlMoeLayer& L, int64_t T, int cap) {
     const int64_t P = T * L.top_k;
-    const int64_t routed = (P + kTileTokens - 1) / kTileTokens + L.n_experts;
-    const int64_t shared = L.shared_gate_up ? (T + kTileTokens - 1) / kTileTokens : 0;
+    const int64_t routed = (P + cap - 1) / cap + L.n_experts;
+    const int64_t shared = L.shared_gate_up ? (T + cap - 1) / cap : 0;
     return static_cast<int>(routed + shared);
 }
 
@@ -701,7 +712,8 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     const int64_t n8 = T * L.hidden / 8;
     k_to_bf16<<<static_cast<unsigned>((n8 + 255) / 256), 256, 0, s>>>(x, w.xb, n8);
     const bool shared = L.shared_gate_up != nullptr;
-    k_tiles<<<1, 256, 0, s>>>(w.offsets, L.n_experts, static_cast<int>(T), shared ? 1 : 0, w.tiles, w.n_tiles);
+    k_tiles<<<1, 256, 0, s>>>(w.offsets, L.n_experts, static_cast<int>(T), shared ? 1 : 0, w.tiles, w.tiles_down,
+                              w.n_tiles);
     PrefillArgs a{};
     a.gate_up = static_cast<const uint8_t*>(L.gate_up);
     a.gate_up_stride = L.gate_up_stride;
@@ -713,6 +725,8 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     a.sorted = w.sorted;
     a.tiles = w.tiles;
     a.n_tiles = w.n_tiles;
+    a.tiles_down = w.tiles_down;
+    a.n_tiles_down = w.n_tiles + 1;
     a.h16 = w.h16;
     a.h_sh16 = w.h_sh16;
     a.o = w.o;
@@ -722,7 +736,8 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     a.sh_inter = shared ? L.shared_inter : 0;
     a.E = L.n_experts;
     a.k = L.top_k;
-    const int tiles8 = (max_tiles(L, T) + kXcds - 1) / kXcds * kXcds;
+    const int tiles8 = (max_tiles(L, T, kTileTokens) + kXcds - 1) / kXcds * kXcds;
+    const int tiles8_down = (max_tiles(L, T, kDownTileTokens) + kXcds - 1) / kXcds * kXcds;
     const int inter_max = shared && L.shared_inter > L.inter ? L.shared_inter : L.inter;
     a.nslab_gate_up = (inter_max + 127) / 128;
     const dim3 g1(static_cast<unsigned>(a.nslab_gate_up * tiles8));
@@ -731,7 +746,7 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
         k_gemm_gate_up<WL_TYPE_Q4_K><<<g1, kGemmThreads, 0, s>>>(a);
     else
         k_gemm_gate_up<WL_TYPE_Q6_K><<<g1, kGemmThreads, 0, s>>>(a);
-    const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8));
+    const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8_down));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
     else
