@@ -298,44 +298,59 @@ __device__ __forceinline__ bf16x8 fragment_q4k(const Q4KRowState& s) {
     return __builtin_bit_cast(bf16x8, p);
 }
 
-// Q6_K order: step KK, group q holds values 32 KK + 8 q + i.
+// Q6_K order: step KK = 2 t + s, group q (h = q >> 1, p = q & 1) holds values 128 h + 32 t + 16 p + 8 s + i. Over a
+// block a group covers 4 scale groups of 16 (scales 8 h + 2 t + p), both nibbles of ql bytes 64 h + 16 p + [0, 16)
+// and 64 h + 32 + 16 p + [0, 16), and qh bytes 32 h + 16 p + [0, 16).
 struct Q6KRowState {
-    uint2 ql[4];   // ql bytes 64h + 32t2 + 8q .. +7, index 2h + t2
-    uint2 qh[2];   // qh bytes 32h + 8q .. +7
-    uint4 sc;      // the 16 int8 scales
+    uint4 ql[2];   // ql bytes 64 h + 32 u + 16 p .. + 15, u = 0, 1
+    uint4 qh;      // qh bytes 32 h + 16 p .. + 15
+    uint2 sc;      // scale bytes 8 h .. 8 h + 7
     float d;
+    float a[4];    // value = a[t] * (q6 - 32), a[t] = d * scale 8 h + 2 t + p
 };
 
 __device__ __forceinline__ void fetch_q6k(const uint8_t* __restrict__ blk, int q, Q6KRowState& s) {
-#pragma unroll
-    for (int m = 0; m < 4; m++) s.ql[m] = load8_a2(blk + 64 * (m >> 1) + 32 * (m & 1) + 8 * q);
-#pragma unroll
-    for (int h = 0; h < 2; h++) s.qh[h] = load8_a2(blk + 128 + 32 * h + 8 * q);
-    // scales: bytes 192..207 from the 4 dwords of their aligned start (bytes 190..205 or 192..207) and, for a block
-    // 2 bytes into a dword, bytes 206..207 as a 16-bit load (the realignment takes only its low half)
+    const int h = q >> 1, p = q & 1;
+    s.ql[0] = load16_a2(blk + 64 * h + 16 * p);
+    s.ql[1] = load16_a2(blk + 64 * h + 32 + 16 * p);
+    s.qh = load16_a2(blk + 128 + 32 * h + 16 * p);
+    // scale bytes 192 + 8 h .. + 7: the dwords of their aligned start and, for a start 2 bytes into a dword, the last
+    // two bytes as a 16-bit load (the realignment takes only its low half; nothing past the block is read)
     uint32_t sh;
-    const uint32_t* p = align_down4(blk + 192, sh);
-    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3];
-    const uint32_t w4 = *reinterpret_cast<const uint16_t*>(blk + 206);
-    s.sc = make_uint4(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
-                      __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh));
+    const uint8_t* sp = blk + 192 + 8 * h;
+    const uint32_t* w = align_down4(sp, sh);
+    const uint32_t w0 = w[0], w1 = w[1];
+    const uint32_t w2 = *reinterpret_cast<const uint16_t*>(sp + 6);
+    s.sc = make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
     s.d = half_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
 }
 
+__device__ __forceinline__ void prepare_q6k(Q6KRowState& s, int q) {
+    // scale 8 h + 2 t + p is byte 2 t + p of sc: word t >> 1, byte 2 (t & 1) + p
+    const uint32_t sh = 8u * static_cast<uint32_t>(q & 1);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t w = (t >> 1) ? s.sc.y : s.sc.x;
+        const int32_t sc = static_cast<int8_t>((w >> (16 * (t & 1) + sh)) & 0xFFu);
+        s.a[t] = s.d * static_cast<float>(sc);
+    }
+}
+
 template <int KK>
-__device__ __forceinline__ bf16x8 fragment_q6k(const Q6KRowState& s, int q) {
-    // values e = 32 kk + 8 q + i: half h = kk / 4, quarter t = kk % 4, scale index e / 16 = 2 kk + q / 2; the
-    // scale word holds indices 4w .. 4w + 3 with w = kk / 2, and q / 2 picks one of the two in this kk's half
-    constexpr int h = KK >> 2, t = KK & 3;
-    const uint2 l4 = s.ql[2 * h + (t & 1)];
-    const uint2 h2 = s.qh[h];
-    constexpr uint32_t lsh = 4 * (t >> 1), hsh = 2 * t;
-    const uint32_t scw = (KK >> 1) == 0 ? s.sc.x : (KK >> 1) == 1 ? s.sc.y : (KK >> 1) == 2 ? s.sc.z : s.sc.w;
-    const uint32_t sbyte = (scw >> (8 * (2 * (KK & 1) + (q >> 1)))) & 0xFFu;
-    const float a = s.d * static_cast<float>(static_cast<int8_t>(sbyte));
-    const float b = -32.0f * a;  // exact: a has at most 18 significant bits
-    const uint32_t v0 = nibbles(l4.x >> lsh) | ((nibbles(h2.x >> hsh) & 0x03030303u) << 4);
-    const uint32_t v1 = nibbles(l4.y >> lsh) | ((nibbles(h2.y >> hsh) & 0x03030303u) << 4);
+__device__ __forceinline__ bf16x8 fragment_q6k(const Q6KRowState& s) {
+    constexpr int t = KK >> 1, sidx = KK & 1;
+    const uint4 l = s.ql[t & 1];
+    const uint32_t l0 = sidx ? l.z : l.x, l1 = sidx ? l.w : l.y;
+    const uint32_t h0 = sidx ? s.qh.z : s.qh.x, h1 = sidx ? s.qh.w : s.qh.y;
+    // 6-bit values: the nibble (low for t < 2) and qh bits 2 t, 2 t + 1 moved to bits 4, 5 of each byte
+    constexpr uint32_t lsh = 4 * (t >> 1);
+    auto six = [&](uint32_t lw, uint32_t hw) {
+        const uint32_t hi = (t == 3 ? (hw >> 2) : (hw << (4 - 2 * t))) & 0x30303030u;
+        return ((lw >> lsh) & 0x0F0F0F0Fu) | hi;
+    };
+    const uint32_t v0 = six(l0, h0), v1 = six(l1, h1);
+    const float a = s.a[t];
+    const float b = -32.0f * a;  // exact: a has at most 19 significant bits
     // a * (q - 32) == fma(a, q, -32 a): the product a * q is exact, so both round the same sum once
     uint4 p;
     affine4(v0, a, b, p.x, p.y);
@@ -357,9 +372,9 @@ template <>
 struct RowState<WL_TYPE_Q6_K> {
     Q6KRowState s;
     __device__ __forceinline__ void fetch(const uint8_t* blk, int q) { fetch_q6k(blk, q, s); }
-    __device__ __forceinline__ void prepare(int) {}
+    __device__ __forceinline__ void prepare(int q) { prepare_q6k(s, q); }
     template <int KK>
-    __device__ __forceinline__ bf16x8 frag(int q) const { return fragment_q6k<KK>(s, q); }
+    __device__ __forceinline__ bf16x8 frag(int) const { return fragment_q6k<KK>(s); }
 };
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -369,14 +384,12 @@ struct RowState<WL_TYPE_Q6_K> {
 //
 // B-fragment of token t = 16 n + lr and the 8 values of slot c (values 8 c .. 8 c + 7): byte address
 // 512 t + 16 (c ^ (lr & 7)) = 512 lr + 16 (c ^ (lr & 7)) + 8192 n.
-// Q6_K order, c = 4 KK + q: with y = q ^ (lr & 7) = 4 y2 + y01 that is 512 lr + 16 y01 + 64 (KK ^ y2) + 8192 n, and
-// 64 (KK ^ y2) = 64 KK + 64 y2 for even KK, 64 KK - 64 y2 for odd KK: two per-lane bases plus a constant offset.
-// Q4_K order, c = 8 q + 4 (KK & 1) + (KK >> 1): a per-lane base for each KK (c ^ (lr & 7) = 8 q + (c & 7) ^ (lr & 7)).
+// Q4_K order, c = 8 q + 4 (KK & 1) + (KK >> 1); Q6_K order, c = 16 h + 4 t + 2 p + s (KK = 2 t + s, q = 2 h + p).
+// In both, XOR with lr & 7 changes only the low 3 bits: a per-lane base for each KK.
 template <int KK>
 constexpr int q4k_slot_low() { return 4 * (KK & 1) + (KK >> 1); }
 
 struct BAddr {
-    uint32_t even, odd;
     uint32_t step[8];
 };
 template <int TYPE>
@@ -394,18 +407,19 @@ __device__ __forceinline__ BAddr b_addr(int lr, int q) {
         ba.step[6] = base + 16u * (q4k_slot_low<6>() ^ y);
         ba.step[7] = base + 16u * (q4k_slot_low<7>() ^ y);
     } else {
-        const int yq = q ^ y, y2 = yq >> 2, base = 512 * lr + 16 * (yq & 3);
-        ba.even = static_cast<uint32_t>(base + 64 * y2);
-        ba.odd = static_cast<uint32_t>(base - 64 * y2);
+        const int h = q >> 1, p = q & 1;
+        const uint32_t base = 512u * lr + 256u * h;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const int t = kk >> 1, sidx = kk & 1;
+            ba.step[kk] = base + 128u * (t >> 1) + 16u * ((4 * (t & 1) + 2 * p + sidx) ^ y);
+        }
     }
     return ba;
 }
 template <int TYPE, int KK>
 __device__ __forceinline__ bf16x8 read_b1(const uint8_t* buf, const BAddr& ba, int n) {
-    if constexpr (TYPE == WL_TYPE_Q4_K)
-        return *reinterpret_cast<const bf16x8*>(buf + ba.step[KK] + 8192 * n);
-    else
-        return *reinterpret_cast<const bf16x8*>(buf + ((KK & 1) ? ba.odd : ba.even) + 64 * KK + 8192 * n);
+    return *reinterpret_cast<const bf16x8*>(buf + ba.step[KK] + 8192 * n);
 }
 template <int TYPE, int NT, int KK>
 __device__ __forceinline__ void read_b(const uint8_t* buf, const BAddr& ba, bf16x8 (&b)[NT]) {
@@ -594,13 +608,16 @@ __device__ __forceinline__ void slab_tile(int nslab, int& slab, int& tile) {
 
 // gate_up: slab = 128-row slab of the intermediate dim; wavefront w: gate rows j0 + 16r + lr (r < kRT / 2)
 // and the matching up rows inter + j0 + ... (r >= kRT / 2), j0 = 128 slab + 8 kRT w. Epilogue h = silu(g) * u -> bf16.
-template <int TYPE>
+// TILE is kTileTokens, or kDownTileTokens (and the down tile list) for Q6_K rows, whose larger row state leaves no
+// registers for a ninth token tile.
+template <int TYPE, int TILE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kTileTokens>()];
+    __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<TILE>()];
     int slab, ti;
     slab_tile(a.nslab_gate_up, slab, ti);
-    if (ti >= a.n_tiles[0]) return;
-    const int4 tile = a.tiles[ti];
+    const int4* tiles = TILE == kTileTokens ? a.tiles : a.tiles_down;
+    if (ti >= (TILE == kTileTokens ? a.n_tiles[0] : a.n_tiles_down[0])) return;
+    const int4 tile = tiles[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
     constexpr int kHalf = kRT / 2;
@@ -610,19 +627,19 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
-    floatx4 acc[kRT][kTileTokens / 16];
+    floatx4 acc[kRT][TILE / 16];
     auto row_ptr = [&](int r, int lr) {
         const int j = j0 + 16 * (r % kHalf) + lr;
         return W + static_cast<int64_t>((r < kHalf ? 0 : inter) + j) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
-    gemm_tile<TYPE, kTileTokens>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
+    gemm_tile<TYPE, TILE>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     uint16_t* out = sh ? a.h_sh16 : a.h16;
 #pragma unroll
     for (int r = 0; r < kHalf; r++) {
 #pragma unroll
-        for (int n = 0; n < kTileTokens / 16; n++) {
+        for (int n = 0; n < TILE / 16; n++) {
             const int t = 16 * n + lr;
             if (t < count) {
                 const int j = j0 + 16 * r + 4 * q;
@@ -740,12 +757,13 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     const int tiles8_down = (max_tiles(L, T, kDownTileTokens) + kXcds - 1) / kXcds * kXcds;
     const int inter_max = shared && L.shared_inter > L.inter ? L.shared_inter : L.inter;
     a.nslab_gate_up = (inter_max + 127) / 128;
-    const dim3 g1(static_cast<unsigned>(a.nslab_gate_up * tiles8));
     // the routed and shared experts share one launch, so their types must agree (checked by prefill_eligible)
     if (L.gate_up_type == WL_TYPE_Q4_K)
-        k_gemm_gate_up<WL_TYPE_Q4_K><<<g1, kGemmThreads, 0, s>>>(a);
+        k_gemm_gate_up<WL_TYPE_Q4_K, kTileTokens>
+            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8)), kGemmThreads, 0, s>>>(a);
     else
-        k_gemm_gate_up<WL_TYPE_Q6_K><<<g1, kGemmThreads, 0, s>>>(a);
+        k_gemm_gate_up<WL_TYPE_Q6_K, kDownTileTokens>
+            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8_down)), kGemmThreads, 0, s>>>(a);
     const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8_down));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
