@@ -54,6 +54,7 @@ struct ExpertArgs {
 
 constexpr int kTileTokens = 144;             // prefill: tokens per gate_up GEMM tile (9 MFMA token tiles)
 constexpr int kDownTileTokens = 128;         // prefill: tokens per down GEMM tile (8 MFMA token tiles)
+constexpr int kDownSlabsMax = 4;            // prefill: most 256-row slabs per down workgroup
 constexpr int kGemvMaxTokens = 8;  // fp32 GEMV experts up to this many tokens, bf16 MFMA GEMMs above (gguf/metal.py:20)
 constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
 
@@ -76,6 +77,7 @@ struct PrefillArgs {
     float* o_sh;             // [T, H]
     int H, inter, sh_inter, E, k;
     int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
+    int down_slabs;          // 256-row slabs per down workgroup
 };
 
 struct Workspace {

@@ -518,12 +518,15 @@ __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
 // add waits of its own for loads issued before it.
 __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 
-// The K loop for NT token tiles. Block kc + 1's row states and LDS tile are requested at the top of iteration kc;
-// the last iteration requests the row states of its own block again (keeping the loop free of branches around the
-// register loads) and no tile.
-template <int TYPE, int TILE, int NT, int NTA, typename RowPtr>
+// The K loop for NT token tiles, over `nitems` row sets (items) one after another: step st is block kc = st % nblocks
+// of item st / nblocks, and the pipeline runs across items. Step st + 1's row states and LDS tile are requested at
+// the top of step st; the last step requests the row states of its own block again (keeping the loop free of
+// branches around the register loads) and no tile. After an item's last block, epi(item, acc) stores it and the
+// accumulators restart from zero.
+template <int TYPE, int TILE, int NT, int NTA, typename RowPtr, typename Epilogue>
 __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][NTA], int nblocks,
-                                          const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr, int lr, int q) {
+                                          int nitems, const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr,
+                                          Epilogue epi, int lr, int q) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
     const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
@@ -531,18 +534,22 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     const BAddr ba = b_addr<TYPE>(lr, q);
     RowState<TYPE> rs[kRT], nx[kRT];
 #pragma unroll
-    for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr), q);
+    for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(0, r, lr), q);
     stage_async<TILE>(lds0, src, rowtab, col, wv, half);
     bf16x8 a0[kRT], a1[kRT], b[NT];
-    for (int kc = 0; kc < nblocks; kc++) {
+    const int nsteps = nitems * nblocks;
+    for (int st = 0; st < nsteps; st++) {
         wait_stage();     // this chunk's LDS tile has landed
         __syncthreads();  // ... for every wavefront, and the other buffer is free
-        const int kn = kc + 1 < nblocks ? kc + 1 : kc;
+        const int sn = st + 1 < nsteps ? st + 1 : st;
+        const int in = sn / nblocks, kn = sn - in * nblocks;
 #pragma unroll
-        for (int r = 0; r < kRT; r++) nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
-        if (kc + 1 < nblocks) stage_async<TILE>((kc & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes,
-                                          rowtab, col, wv, half);
-        const uint8_t* buf = bufs[kc & 1];
+        for (int r = 0; r < kRT; r++)
+            nx[r].fetch(row_ptr(in, r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
+        if (st + 1 < nsteps)
+            stage_async<TILE>((st & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes, rowtab, col, wv,
+                              half);
+        const uint8_t* buf = bufs[st & 1];
         read_b<TYPE, NT, 0>(buf, ba, b);
         // the block's first fragments are decoded here, after the wait for every outstanding load, rather than in
         // the previous iteration's last step: the row-state loads get a whole iteration to land
@@ -561,21 +568,29 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
         gemm_step<TYPE, NT, 7, NTA>(buf, ba, rs, acc, a1, b, a0, q);
 #pragma unroll
         for (int r = 0; r < kRT; r++) rs[r] = nx[r];
+        const int item = st / nblocks;
+        if (st - item * nblocks == nblocks - 1) {
+            epi(item, acc);
+#pragma unroll
+            for (int r = 0; r < kRT; r++)
+#pragma unroll
+                for (int n = 0; n < NTA; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
     }
     wait_stage();
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // The GEMM core: a workgroup of kGemmWaves wavefronts, each owning kRT row tiles of 16 (rows given by
-// row_ptr(r, lr)) and the tile's up to TILE tokens as NT token tiles of 16 (NT = TILE / 16, 8 or 4, the fewest
-// that cover `count`). Per K chunk of 256 values (one block per row) the activations sit in LDS, double-buffered, and each
-// of the 8 32-value steps decodes kRT A-fragments and runs kRT x NT MFMAs. src_row(t) is token t's row in src
-// ([*, ld] bf16); rows past count load token 0's (their results are never stored).
-template <int TYPE, int TILE, typename RowPtr, typename SrcRow>
+// row_ptr(item, r, lr), for nitems row sets one after another) and the tile's up to TILE tokens as NT token tiles of
+// 16 (NT = TILE / 16, 8 or 4, the fewest that cover `count`). Per K chunk of 256 values (one block per row) the
+// activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes kRT A-fragments and runs
+// kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in src ([*, ld] bf16);
+// rows past count load token 0's (their results are never stored).
+template <int TYPE, int TILE, typename RowPtr, typename SrcRow, typename Epilogue>
 __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][TILE / 16],
-                                          int nblocks,
-                                          int count, const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
-                                          RowPtr row_ptr) {
+                                          int nblocks, int nitems, int count, const uint16_t* __restrict__ src,
+                                          int64_t ld, SrcRow src_row, RowPtr row_ptr, Epilogue epi) {
     constexpr int NTA = TILE / 16;
     __shared__ __attribute__((aligned(16))) uint32_t rowtab[TILE];
     const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
@@ -588,11 +603,11 @@ __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     __syncthreads();
     const uint8_t* s8 = uniform_ptr(reinterpret_cast<const uint8_t*>(src));
     if (NTA > 8 && count > 128)
-        gemm_loop<TYPE, TILE, NTA, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+        gemm_loop<TYPE, TILE, NTA, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
     else if (count > 64)
-        gemm_loop<TYPE, TILE, 8, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+        gemm_loop<TYPE, TILE, 8, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
     else
-        gemm_loop<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+        gemm_loop<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its own L2. slab_tile maps the linear
@@ -628,64 +643,72 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
     floatx4 acc[kRT][TILE / 16];
-    auto row_ptr = [&](int r, int lr) {
+    auto row_ptr = [&](int, int r, int lr) {
         const int j = j0 + 16 * (r % kHalf) + lr;
         return W + static_cast<int64_t>((r < kHalf ? 0 : inter) + j) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
-    gemm_tile<TYPE, TILE>(bufs, acc, nb, count, a.xb, a.H, src_row, row_ptr);
-    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     uint16_t* out = sh ? a.h_sh16 : a.h16;
+    auto epi = [&](int, floatx4 (&acc)[kRT][TILE / 16]) {
+        const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
 #pragma unroll
-    for (int r = 0; r < kHalf; r++) {
+        for (int r = 0; r < kHalf; r++) {
 #pragma unroll
-        for (int n = 0; n < TILE / 16; n++) {
-            const int t = 16 * n + lr;
-            if (t < count) {
-                const int j = j0 + 16 * r + 4 * q;
-                const floatx4 g = acc[r][n], u = acc[r + kHalf][n];
-                const uint2 v = make_uint2(pack2(silu(g[0]) * u[0], silu(g[1]) * u[1]),
-                                           pack2(silu(g[2]) * u[2], silu(g[3]) * u[3]));
-                *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j) = v;
+            for (int n = 0; n < TILE / 16; n++) {
+                const int t = 16 * n + lr;
+                if (t < count) {
+                    const int j = j0 + 16 * r + 4 * q;
+                    const floatx4 g = acc[r][n], u = acc[r + kHalf][n];
+                    const uint2 v = make_uint2(pack2(silu(g[0]) * u[0], silu(g[1]) * u[1]),
+                                               pack2(silu(g[2]) * u[2], silu(g[3]) * u[3]));
+                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j) = v;
+                }
             }
         }
-    }
+    };
+    gemm_tile<TYPE, TILE>(bufs, acc, nb, 1, count, a.xb, a.H, src_row, row_ptr, epi);
 }
 
-// down: slab = 256-row slab of the hidden dim; wavefront w: rows r0 + 16 kRT w + 16 r + lr. o fp32 by position.
-// Its tiles hold at most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts within 256 registers).
+// down: a workgroup takes a.down_slabs consecutive 256-row slabs of the hidden dim (one pipeline across them); for
+// slab item, wavefront w has rows 256 (slab0 + item) + 16 kRT w + 16 r + lr. o fp32 by position. Its tiles hold at
+// most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts within 256 registers).
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kDownTileTokens>()];
-    int slab, ti;
-    slab_tile(a.H / 256, slab, ti);
+    int group, ti;
+    slab_tile(a.H / 256 / a.down_slabs, group, ti);
     if (ti >= a.n_tiles_down[0]) return;
     const int4 tile = a.tiles_down[ti];
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
-    const int row0 = slab * 256 + 16 * kRT * (threadIdx.x >> 6);
+    const int row0 = group * a.down_slabs * 256 + 16 * kRT * (threadIdx.x >> 6);
     const uint8_t* W = sh ? a.sh_down : a.down + static_cast<int64_t>(tile.x) * a.down_stride;
     const int nb = inter / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int pos0 = tile.y, count = tile.z;
     floatx4 acc[kRT][kDownTileTokens / 16];
-    auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>(row0 + 16 * r + lr) * rs; };
+    auto row_ptr = [&](int item, int r, int lr) {
+        return W + static_cast<int64_t>(row0 + 256 * item + 16 * r + lr) * rs;
+    };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
-    gemm_tile<TYPE, kDownTileTokens>(bufs, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
-    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
     float* out = sh ? a.o_sh : a.o;
+    auto epi = [&](int item, floatx4 (&acc)[kRT][kDownTileTokens / 16]) {
+        const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
 #pragma unroll
-    for (int r = 0; r < kRT; r++) {
+        for (int r = 0; r < kRT; r++) {
 #pragma unroll
-        for (int n = 0; n < kDownTileTokens / 16; n++) {
-            const int t = 16 * n + lr;
-            if (t < count) {
-                const floatx4 v = acc[r][n];
-                *reinterpret_cast<float4*>(out + static_cast<int64_t>(pos0 + t) * a.H + row0 + 16 * r + 4 * q) =
-                    make_float4(v[0], v[1], v[2], v[3]);
+            for (int n = 0; n < kDownTileTokens / 16; n++) {
+                const int t = 16 * n + lr;
+                if (t < count) {
+                    const floatx4 v = acc[r][n];
+                    *reinterpret_cast<float4*>(out + static_cast<int64_t>(pos0 + t) * a.H + row0 + 256 * item +
+                                               16 * r + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
+                }
             }
         }
-    }
+    };
+    gemm_tile<TYPE, kDownTileTokens>(bufs, acc, nb, a.down_slabs, count, sh ? a.h_sh16 : a.h16, inter, src_row,
+                                     row_ptr, epi);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -723,6 +746,16 @@ int max_tiles(const WlMoeLayer& L, int64_t T, int cap) {
     const int64_t routed = (P + cap - 1) / cap + L.n_experts;
     const int64_t shared = L.shared_gate_up ? (T + cap - 1) / cap : 0;
     return static_cast<int>(routed + shared);
+}
+
+// 256-row slabs per down workgroup: several when there are enough tiles to fill the GPU with fewer workgroups, so
+// that each pays its pipeline start once for several slabs.
+static int down_slabs(const WlMoeLayer& L, int64_t T) {
+    const int nslab = L.hidden / 256;
+    const int64_t tiles = max_tiles(L, T, kDownTileTokens) - L.n_experts;  // about the full tiles
+    int p = 1;
+    while (p < kDownSlabsMax && nslab % (2 * p) == 0 && tiles * nslab / (2 * p) >= 4 * 256) p *= 2;
+    return p;
 }
 
 int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s) {
@@ -764,7 +797,8 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     else
         k_gemm_gate_up<WL_TYPE_Q6_K, kDownTileTokens>
             <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8_down)), kGemmThreads, 0, s>>>(a);
-    const dim3 g2(static_cast<unsigned>(L.hidden / 256 * tiles8_down));
+    a.down_slabs = down_slabs(L, T);
+    const dim3 g2(static_cast<unsigned>(L.hidden / 256 / a.down_slabs * tiles8_down));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
     else
