@@ -521,7 +521,8 @@ __device__ __forceinline__ void wait_stage() { __builtin_amdgcn_s_waitcnt(0); }
 // The K loop for NT token tiles, over `nitems` row sets (items) one after another: step st is block kc = st % nblocks
 // of item st / nblocks, and the pipeline runs across items. Step st + 1's row states and LDS tile are requested at
 // the top of step st; the last step requests the row states of its own block again (keeping the loop free of
-// branches around the register loads) and no tile. After an item's last block, epi(item, acc) stores it and the
+// branches around the register loads) and no tile. With at most two blocks, both chunks stay in LDS (chunk kc in
+// buffer kc) and are staged once for all items. After an item's last block, epi(item, acc) stores it and the
 // accumulators restart from zero.
 template <int TYPE, int TILE, int NT, int NTA, typename RowPtr, typename Epilogue>
 __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][NTA], int nblocks,
@@ -546,10 +547,11 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
 #pragma unroll
         for (int r = 0; r < kRT; r++)
             nx[r].fetch(row_ptr(in, r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
-        if (st + 1 < nsteps)
-            stage_async<TILE>((st & 1) ? lds0 : lds1, src + static_cast<int64_t>(kn) * kTileRowBytes, rowtab, col, wv,
-                              half);
-        const uint8_t* buf = bufs[st & 1];
+        const bool resident = nblocks <= 2;
+        if (st + 1 < nsteps && (!resident || sn < nblocks))
+            stage_async<TILE>((resident ? kn : ((st + 1) & 1)) ? lds1 : lds0,
+                              src + static_cast<int64_t>(kn) * kTileRowBytes, rowtab, col, wv, half);
+        const uint8_t* buf = bufs[resident ? st - (st / nblocks) * nblocks : (st & 1)];
         read_b<TYPE, NT, 0>(buf, ba, b);
         // the block's first fragments are decoded here, after the wait for every outstanding load, rather than in
         // the previous iteration's last step: the row-state loads get a whole iteration to land
@@ -749,12 +751,13 @@ int max_tiles(const WlMoeLayer& L, int64_t T, int cap) {
 }
 
 // 256-row slabs per down workgroup: several when there are enough tiles to fill the GPU with fewer workgroups, so
-// that each pays its pipeline start once for several slabs.
+// that each pays its pipeline start (and, with inter <= 512, its activation staging) once for several slabs.
+constexpr int64_t kDownMinGroups = 1024;
 static int down_slabs(const WlMoeLayer& L, int64_t T) {
     const int nslab = L.hidden / 256;
     const int64_t tiles = max_tiles(L, T, kDownTileTokens) - L.n_experts;  // about the full tiles
     int p = 1;
-    while (p < kDownSlabsMax && nslab % (2 * p) == 0 && tiles * nslab / (2 * p) >= 4 * 256) p *= 2;
+    while (p < kDownSlabsMax && nslab % (2 * p) == 0 && tiles * nslab / (2 * p) >= kDownMinGroups) p *= 2;
     return p;
 }
 
