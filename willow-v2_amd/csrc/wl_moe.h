@@ -115,7 +115,8 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
 int zero_sync(void* workspace, hipStream_t s);
 bool prefill_eligible(const WlMoeLayer& L, int64_t T);
 int max_tiles(const WlMoeLayer& L, int64_t T, int cap);
-int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s);
+int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
+                        hipStream_t s);
 int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s);
 
 }  // namespace wl

@@ -20,7 +20,8 @@ namespace wl {
 // spread over the banks), and lane (row 4 w + lane / 16, segment j = lane % 16) chains the TT tokens' partials of
 // segment 16 c + j from its row's 64 weights, loaded once. The partials go to LDS; thread (token u, row r) then
 // adds the chunk's partials to its output's running total, left to right. A ragged last token group recomputes its
-// last token for the missing ones and stores nothing for them.
+// last token for the missing ones and stores nothing for them. With xb, the first row group's workgroups also store
+// the tokens' values as bf16 (round to nearest even) while staging them, for the MFMA path.
 // The shared-expert gate is row E (weight vector shared_gate, no bias); its output is sigmoid(logit).
 constexpr int kRouterChunkSegs = 16;
 constexpr int kRouterPad = kRouterSeg + 4;
@@ -29,7 +30,8 @@ template <int TT>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ w,
                                                 const float* __restrict__ bias,
                                                 const float* __restrict__ shared_gate, int T, int H, int E,
-                                                float* __restrict__ logits, float* __restrict__ sg) {
+                                                float* __restrict__ logits, float* __restrict__ sg,
+                                                uint16_t* __restrict__ xb) {
     __shared__ __attribute__((aligned(16))) float xs[TT][kRouterChunkSegs * kRouterPad];
     __shared__ float part[16 * TT][kRouterChunkSegs + 1];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -49,9 +51,12 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
             const int f = tid + 256 * it;  // float4 f of the chunk: token f / 256, segment (f / 16) % 16, i = f % 16
             const int u = f >> 8, sg4 = (f >> 4) & 15, i = f & 15;
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (c + sg4 < nseg)
-                v = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(min(t0 + u, T - 1)) * H +
-                                                     (c + sg4) * kRouterSeg + 4 * i);
+            if (c + sg4 < nseg) {
+                const int64_t at = static_cast<int64_t>(min(t0 + u, T - 1)) * H + (c + sg4) * kRouterSeg + 4 * i;
+                v = *reinterpret_cast<const float4*>(x + at);
+                if (xb && blockIdx.x == 0 && t0 + u < T)
+                    *reinterpret_cast<uint2*>(xb + at) = make_uint2(pack2(v.x, v.y), pack2(v.z, v.w));
+            }
             *reinterpret_cast<float4*>(&xs[u][sg4 * kRouterPad + 4 * i]) = v;
         }
         __syncthreads();
@@ -222,9 +227,25 @@ __device__ void write_active(const int32_t* counts, int E, int32_t* __restrict__
 }
 
 // One chunk (T <= kSortChunk): everything in one workgroup.
+// With tiles non-null (the MFMA path), the sort's single-workgroup stage also writes the GEMMs' tile lists.
+struct TileOut {
+    int4* tiles;
+    int4* tiles_down;
+    int32_t* n_tiles;
+    int with_shared;
+};
+
+__device__ __forceinline__ void write_tiles(const TileOut& to, const int32_t* offsets, int E, int T) {
+    __shared__ int scan[2][256];
+    __syncthreads();  // offsets[] written by this workgroup are visible to all of it
+    tile_list(offsets, E, T, to.with_shared, kTileTokens, to.tiles, to.n_tiles, scan);
+    tile_list(offsets, E, T, to.with_shared, kDownTileTokens, to.tiles_down, to.n_tiles + 1, scan);
+}
+
 __global__ __launch_bounds__(256) void k_sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
                                                     int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                                    int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos) {
+                                                    int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos,
+                                                    TileOut to) {
     extern __shared__ uint32_t smem[];
     uint32_t* bits = smem;
     int32_t* counts = reinterpret_cast<int32_t*>(bits + E * kSortWords);
@@ -246,6 +267,7 @@ __global__ __launch_bounds__(256) void k_sort_small(const int32_t* __restrict__ 
         sorted[pos] = q;
         pair_pos[q] = pos;
     }
+    if (to.tiles) write_tiles(to, offsets, E, T);
 }
 
 // Many chunks: per-chunk ranks and counts, then one scan, then the scatter.
@@ -269,7 +291,8 @@ __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ i
 }
 
 __global__ __launch_bounds__(256) void k_sort_scan(int T, int k, int E, int nchunks, int32_t* __restrict__ hist,
-                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ active) {
+                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                                   TileOut to) {
     extern __shared__ uint32_t smem[];
     int32_t* counts = reinterpret_cast<int32_t*>(smem);
     int32_t* offs = counts + E;
@@ -295,6 +318,7 @@ __global__ __launch_bounds__(256) void k_sort_scan(int T, int k, int E, int nchu
     }
     if (tid == 0) offsets[E] = T * k;
     write_active(counts, E, active, flags, scratch);
+    if (to.tiles) write_tiles(to, offsets, E, T);
 }
 
 __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int T, int k, int E,
@@ -570,7 +594,8 @@ int check_layer(const WlMoeLayer* L) {
     return WL_OK;
 }
 
-static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s) {
+static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
+                         hipStream_t s) {
     const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
     const int rows = L.n_experts + (shared_gate ? 1 : 0);
     const int grid = (rows + 1) / 2;
@@ -578,7 +603,7 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
         k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
     else
         k_router<8><<<dim3(static_cast<unsigned>((rows + 15) / 16), static_cast<unsigned>((T + 7) / 8)), 256, 0, s>>>(
-            x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg);
+            x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg, xb);
     return launch_status();
 }
 
@@ -599,18 +624,21 @@ static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int3
     return launch_status();
 }
 
-static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* ids, int64_t T, hipStream_t s) {
+static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* ids, int64_t T, bool tiles,
+                       hipStream_t s) {
     const int E = L.n_experts, k = L.top_k;
+    const TileOut to{tiles ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0};
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
     const size_t scan_lds = sizeof(int32_t) * (3 * E + 2 * 256 + 1);
     if (nchunks == 1) {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + scan_lds;
-        k_sort_small<<<1, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted, w.pair_pos);
+        k_sort_small<<<1, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted, w.pair_pos,
+                                         to);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
         k_sort_hist<<<nchunks, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
         k_sort_scan<<<1, 256, scan_lds + sizeof(int32_t) * E, s>>>(static_cast<int>(T), k, E, nchunks, w.hist,
-                                                                   w.offsets, w.active);
+                                                                   w.offsets, w.active, to);
         const int64_t P = T * k;
         k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(ids, static_cast<int>(T), k, E, w.rank,
                                                                           w.hist, w.sorted, w.pair_pos);
@@ -749,8 +777,8 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
     if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16) return WL_EINVAL_ALIGN;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(*layer, x, tokens, logits, shared_gate_out, s)
-                                         : launch_router(*layer, x, tokens, logits, shared_gate_out, s);
+    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(*layer, x, tokens, logits, shared_gate_out, nullptr, s)
+                                         : launch_router(*layer, x, tokens, logits, shared_gate_out, nullptr, s);
     if (rc) return rc;
     return launch_topk(*layer, logits, tokens, ids, weights, nullptr, s);
 }
@@ -786,17 +814,19 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
     auto mark = record;
     mark(0);
-    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, s)
-                                         : launch_router(L, x, tokens, w.logits, sg, s);
+    // on the MFMA path the router also writes x as bf16 and the sort also writes the GEMM tile lists
+    const bool mfma = prefill_eligible(L, tokens);
+    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s)
+                                         : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
     if (rc) return rc;
     mark(1);
     rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
     if (rc) return rc;
     mark(2);
-    rc = launch_sort(L, w, w.ids, tokens, s);
+    rc = launch_sort(L, w, w.ids, tokens, mfma, s);
     if (rc) return rc;
     mark(3);
-    if (prefill_eligible(L, tokens)) {  // bf16 MFMA GEMMs (gate_up + SwiGLU in one stage, down in the next)
+    if (mfma) {  // bf16 MFMA GEMMs (gate_up + SwiGLU in one stage, down in the next)
         rc = launch_prefill_experts(L, x, tokens, w, s);
         if (rc) return rc;
         mark(4);

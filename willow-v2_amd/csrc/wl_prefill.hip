@@ -6,14 +6,15 @@
 // registers (fp32 value, rounded to bf16 like Tensor.to(torch.bfloat16)), while the tokens' activations (bf16) are
 // staged in LDS as the B-operand. Accumulation is fp32.
 //
-//   k_router_mfma    logits for many tokens in the router's fixed order (64-value FMA segments, added left to right)
-//   k_to_bf16        x -> bf16
-//   k_tiles          per-expert tiles of up to 128 tokens (sorted positions), then the shared expert's
+//   k_router_mfma    logits for many tokens in the router's fixed order (64-value FMA segments, added left to
+//                    right); also writes x as bf16 (the small-batch router in wl_moe.hip does the same)
+//   (sort)           the sort's single-workgroup stage writes the tile lists (tile_list): per-expert tiles of
+//                    sorted positions, then the shared expert's, of at most 144 (gate_up) and 128 (down) tokens
 //   k_gemm_gate_up   per (tile, 128 intermediate rows): gate and up rows together, epilogue h = silu(g) * u -> bf16
 //   k_gemm_down      per (tile, 256 output rows): o = down h, fp32, by sorted position (combined by k_combine)
 //
 // MFMA 16x16x32 bf16 operand layout (wave64): lane l holds A[l % 16][8 (l / 16) + i], B[8 (l / 16) + i][l % 16],
-// and C[4 (l / 16) + i][l % 16], i < 8 (A, B) or < 4 (C). A wavefront covers kRT row tiles x 8 token tiles.
+// and C[4 (l / 16) + i][l % 16], i < 8 (A, B) or < 4 (C). A wavefront covers kRT row tiles x up to 9 token tiles.
 #include <hip/hip_runtime.h>
 
 #include "wl_common.h"
@@ -36,14 +37,6 @@ constexpr int tile_bytes() { return TILE * kTileRowBytes; }  // one LDS buffer: 
 constexpr int kRT = 2;
 constexpr int kGemmWaves = 16 / kRT;
 constexpr int kGemmThreads = 64 * kGemmWaves;
-
-typedef float floatx2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two floats -> two bf16 (round to nearest even, like Tensor.to(torch.bfloat16)) in one v_cvt_pk_bf16_f32.
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{a, b}, bf16x2));
-}
 
 // 8 bytes from a 2-byte-aligned address: 3 aligned dwords, realigned. Reads [p & ~3, (p & ~3) + 12), within
 // [p - 2, p + 12); all three loads are unconditional so that no branch splits the wavefront.
@@ -71,7 +64,8 @@ template <int TM>
 __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x, const float* __restrict__ w,
                                                      const float* __restrict__ bias,
                                                      const float* __restrict__ shared_gate, int T, int H, int E,
-                                                     float* __restrict__ logits, float* __restrict__ sg) {
+                                                     float* __restrict__ logits, float* __restrict__ sg,
+                                                     uint16_t* __restrict__ xb) {
     constexpr int kTok = 32 * TM;              // tokens per workgroup
     constexpr int kXq = kTok * 16 / 256;       // float4 loads per thread per segment (tokens)
     __shared__ __attribute__((aligned(16))) float xs[4 * kTok * kRmRow];
@@ -112,6 +106,9 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
 #pragma unroll
         for (int q = 0; q < kXq; q++) {
             const int rr = (tid + 256 * q) >> 4;
+            if (xb && blockIdx.y == 0 && t0 + rr < T)  // x as bf16 for the MFMA GEMMs, written once per token
+                *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + sgi * kRouterSeg + 4 * s4) =
+                    make_uint2(pack2(xn[q].x, xn[q].y), pack2(xn[q].z, xn[q].w));
             xs[(0 * kTok + rr) * kRmRow + s4] = xn[q].x;
             xs[(1 * kTok + rr) * kRmRow + s4] = xn[q].y;
             xs[(2 * kTok + rr) * kRmRow + s4] = xn[q].z;
@@ -177,61 +174,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
         }
 }
 
-// x fp32 -> bf16, 8 values per thread.
-__global__ __launch_bounds__(256) void k_to_bf16(const float* __restrict__ x, uint16_t* __restrict__ xb, int64_t n8) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= n8) return;
-    const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
-    const float4 b = reinterpret_cast<const float4*>(x)[2 * i + 1];
-    reinterpret_cast<uint4*>(xb)[i] = make_uint4(pack2(a.x, a.y), pack2(a.z, a.w), pack2(b.x, b.y), pack2(b.z, b.w));
-}
 
-// Tiles: each routed expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles of at
-// most `cap` tokens; tiles[i] = (expert, first position or token, count), n_tiles[0] = how many. One workgroup of
-// 256 threads, thread i owning experts 4i .. 4i + 3 (E <= 1024): tile counts, an exclusive scan of them across the
-// workgroup, then each thread writes its experts' tiles in expert order. Two lists, for the two GEMMs' tile sizes.
-__device__ void tile_list(const int32_t* __restrict__ offsets, int E, int T, int with_shared, int cap,
-                          int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int (&scan)[2][256]) {
-    const int tid = threadIdx.x;
-    int mine = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * tid + i;
-        mine += e < E ? (offsets[e + 1] - offsets[e] + cap - 1) / cap : 0;
-    }
-    int cur = 0;
-    __syncthreads();  // scan is free (a previous list's reads are done)
-    scan[0][tid] = mine;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        const int v = scan[cur][tid] + (tid >= off ? scan[cur][tid - off] : 0);
-        scan[cur ^ 1][tid] = v;
-        cur ^= 1;
-        __syncthreads();
-    }
-    int n = scan[cur][tid] - mine;  // tiles before this thread's experts
-    const int total = scan[cur][255];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * tid + i;
-        if (e >= E) break;
-        const int b = offsets[e], c = offsets[e + 1] - b;
-        for (int p = 0; p < c; p += cap) tiles[n++] = make_int4(e, b + p, min(cap, c - p), 0);
-    }
-    int m = total;
-    if (with_shared)
-        for (int p = tid * cap; p < T; p += 256 * cap) tiles[total + p / cap] = make_int4(E, p, min(cap, T - p), 0);
-    if (with_shared) m += (T + cap - 1) / cap;
-    if (tid == 0) n_tiles[0] = m;
-}
-
-__global__ __launch_bounds__(256) void k_tiles(const int32_t* __restrict__ offsets, int E, int T, int with_shared,
-                                               int4* __restrict__ tiles, int4* __restrict__ tiles_down,
-                                               int32_t* __restrict__ n_tiles) {
-    __shared__ int scan[2][256];
-    tile_list(offsets, E, T, with_shared, kTileTokens, tiles, n_tiles, scan);
-    tile_list(offsets, E, T, with_shared, kDownTileTokens, tiles_down, n_tiles + 1, scan);
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // A-operand decoders. At 32-value step KK of a 256-value block, lane group q (lanes 16 q .. 16 q + 15, one row
@@ -726,7 +669,8 @@ __global__ __launch_bounds__(256) void k_router_sg(const float* __restrict__ x, 
     if ((lane & 31) == 0 && valid) sg[t] = sigmoid(total);
 }
 
-int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, hipStream_t s) {
+int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
+                        hipStream_t s) {
     const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
     // with whole 64-row tiles of experts the shared gate gets its own small kernel instead of a 1-row tile
     const bool separate = shared_gate && L.n_experts % 64 == 0;
@@ -736,7 +680,7 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
     k_router_mfma<kRouterMfmaTM><<<dim3(static_cast<unsigned>((T + 32 * kRouterMfmaTM - 1) / (32 * kRouterMfmaTM)),
                                         rtiles),
                                    256, 0, s>>>(x, L.router, L.router_bias, tiled_gate, static_cast<int>(T), L.hidden,
-                                                L.n_experts, logits, sg);
+                                                L.n_experts, logits, sg, xb);
     if (separate)
         k_router_sg<<<static_cast<unsigned>((T + 7) / 8), 256, 0, s>>>(x, shared_gate, static_cast<int>(T),
                                                                        L.hidden, sg);
@@ -762,11 +706,7 @@ static int down_slabs(const WlMoeLayer& L, int64_t T) {
 }
 
 int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s) {
-    const int64_t n8 = T * L.hidden / 8;
-    k_to_bf16<<<static_cast<unsigned>((n8 + 255) / 256), 256, 0, s>>>(x, w.xb, n8);
     const bool shared = L.shared_gate_up != nullptr;
-    k_tiles<<<1, 256, 0, s>>>(w.offsets, L.n_experts, static_cast<int>(T), shared ? 1 : 0, w.tiles, w.tiles_down,
-                              w.n_tiles);
     PrefillArgs a{};
     a.gate_up = static_cast<const uint8_t*>(L.gate_up);
     a.gate_up_stride = L.gate_up_stride;
