@@ -481,7 +481,11 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
     }
 }
 
-// y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r].
+// y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r]. For k <= 8
+// every index and weight of the token is loaded first and then every o row, so the loads overlap instead of forming
+// k dependent chains; the sum is the same in both forms.
+constexpr int kCombineUnroll = 8;
+
 __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int32_t* __restrict__ corder,
                                                  const int32_t* __restrict__ pair_pos,
                                                  const float* __restrict__ wts, const float* __restrict__ o,
@@ -492,14 +496,9 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
     if (i >= static_cast<int64_t>(T) * h4) return;
     const int t = static_cast<int>(i / h4);
     const int r = static_cast<int>(i - static_cast<int64_t>(t) * h4) * 4;
+    const int P = T * k;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int n = 0; n < k; n++) {
-        const int s = corder[static_cast<int64_t>(t) * k + n];
-        const int64_t q = static_cast<int64_t>(t) * k + s;
-        const int pos = pair_pos[q];
-        if (pos < 0 || pos >= T * k) continue;  // never true for ids from k_topk; guards caller-supplied ids
-        const float wv = wts[q];
-        const float4 ov = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos) * H + r);
+    auto add = [&](int n, float wv, float4 ov) {
         if (n == 0) {
             acc = make_float4(wv * ov.x, wv * ov.y, wv * ov.z, wv * ov.w);
         } else {
@@ -507,6 +506,36 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             acc.y += wv * ov.y;
             acc.z += wv * ov.z;
             acc.w += wv * ov.w;
+        }
+    };
+    if (k <= kCombineUnroll) {
+        int pos[kCombineUnroll];
+        float wv[kCombineUnroll];
+#pragma unroll
+        for (int n = 0; n < kCombineUnroll; n++) {
+            pos[n] = -1;
+            wv[n] = 0.0f;
+            if (n < k) {
+                const int64_t q = static_cast<int64_t>(t) * k + corder[static_cast<int64_t>(t) * k + n];
+                pos[n] = pair_pos[q];
+                wv[n] = wts[q];
+            }
+        }
+        float4 ov[kCombineUnroll];
+#pragma unroll
+        for (int n = 0; n < kCombineUnroll; n++)
+            if (n < k && pos[n] >= 0 && pos[n] < P)  // never false for ids from k_topk; guards caller-supplied ids
+                ov[n] = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos[n]) * H + r);
+#pragma unroll
+        for (int n = 0; n < kCombineUnroll; n++)
+            if (n < k && pos[n] >= 0 && pos[n] < P) add(n, wv[n], ov[n]);
+    } else {
+        for (int n = 0; n < k; n++) {
+            const int s = corder[static_cast<int64_t>(t) * k + n];
+            const int64_t q = static_cast<int64_t>(t) * k + s;
+            const int pos = pair_pos[q];
+            if (pos < 0 || pos >= P) continue;
+            add(n, wts[q], *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos) * H + r));
         }
     }
     if (o_sh) {
