@@ -48,26 +48,30 @@ def sigmoid(v: np.ndarray) -> np.ndarray:
 
 
 def expert_ffn(x: np.ndarray, gate_up_w: np.ndarray, down_w: np.ndarray, inter: int, dtype=np.float32,
-               bf16_operands: bool = False) -> np.ndarray:
+               bf16_operands: bool = False, bf16_output: bool = False) -> np.ndarray:
     """down(silu(gate x) * (up x)) for x [n, hidden], with dequantized fused gate_up [2*inter, hidden] (gate rows
     first) and down [hidden, inter] (engines/base.py:99-102, :567-571). bf16_operands rounds x, the weights and
     the SwiGLU output to bf16 before each product, as a bf16 matmul of dequantized weights does
-    (gguf/metal.py:407)."""
+    (gguf/metal.py:407); bf16_output rounds the result to bf16 too, as that F.linear returns it."""
     if bf16_operands:
         x, gate_up_w, down_w = round_bf16(x), round_bf16(gate_up_w), round_bf16(down_w)
     gu = x.astype(dtype) @ gate_up_w.astype(dtype).T
     h = silu(gu[:, :inter]) * gu[:, inter:]
     if bf16_operands:
         h = round_bf16(h.astype(np.float32)).astype(dtype)
-    return h @ down_w.astype(dtype).T
+    out = h @ down_w.astype(dtype).T
+    if bf16_output:
+        out = round_bf16(out.astype(np.float32)).astype(dtype)
+    return out
 
 
 def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False, return_routing: bool = False,
-          bf16_shared: bool = None):
+          bf16_shared: bool = None, bf16_outputs: bool = False):
     """The whole MoE layer for x fp32 [T, hidden]; lw is a layer dict as synth.moe_layer builds it. Returns
     y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values). bf16_operands
     rounds the routed experts' operands to bf16 (expert_ffn); bf16_shared does the same for the shared expert
-    (default: as bf16_operands)."""
+    (default: as bf16_operands). bf16_outputs also rounds each expert's output to bf16 (the shared expert's only
+    with bf16_shared); the weighted sum stays fp32."""
     if bf16_shared is None:
         bf16_shared = bf16_operands
     hidden, inter, experts = lw["hidden"], lw["inter"], lw["experts"]
@@ -79,14 +83,14 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False
         token_idx, slot = np.nonzero(ids == expert)
         gate_up_w = dequantize_matrix(lw["gate_up"][expert], lw["gate_up_type"], 2 * inter, hidden)
         down_w = dequantize_matrix(lw["down"][expert], lw["down_type"], hidden, inter)
-        h = expert_ffn(x[token_idx], gate_up_w, down_w, inter, dtype, bf16_operands)
+        h = expert_ffn(x[token_idx], gate_up_w, down_w, inter, dtype, bf16_operands, bf16_outputs)
         np.add.at(y, token_idx, h * weights[token_idx, slot, None].astype(dtype))
     shared_gate = None
     if lw.get("shared_gate_up") is not None:
         s_inter = lw["shared_inter"]
         gate_up_w = dequantize_matrix(lw["shared_gate_up"], lw["shared_gate_up_type"], 2 * s_inter, hidden)
         down_w = dequantize_matrix(lw["shared_down"], lw["shared_down_type"], hidden, s_inter)
-        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype, bf16_shared)
+        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype, bf16_shared, bf16_outputs and bf16_shared)
         if lw.get("shared_gate") is not None:
             z = cref.router_logits(x, lw["shared_gate"][None, :])[:, 0]
             shared_gate = sigmoid(z.astype(np.float32)).astype(np.float32)

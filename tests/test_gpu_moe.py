@@ -184,11 +184,12 @@ def test_layer_variants(hip, variant):
 
 
 def check_prefill(hip, layer, lw, x, label, tol=TOL):
-    """The MFMA path against the oracle with the same bf16 roundings (x, dequantized weights and the SwiGLU
-    output to bf16; fp32 products and sums), and against the all-fp32 oracle within bf16 accuracy."""
+    """The MFMA path against the oracle with the same bf16 roundings (x, dequantized weights, the SwiGLU output
+    and each expert's output to bf16, as the reference's bf16 F.linear path; fp32 products and sums), and against
+    the all-fp32 oracle within bf16 accuracy."""
     print(f"[prefill] {label}: T={x.shape[0]}", flush=True)
     y, ids, wts = run_layer(hip, layer, x)
-    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, bf16_operands=True, return_routing=True)
+    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, bf16_operands=True, bf16_outputs=True, return_routing=True)
     np.testing.assert_array_equal(ids, ids_ref)
     np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
     err = moe_ref.rel_err(y, y_b)

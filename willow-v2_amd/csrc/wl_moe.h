@@ -73,8 +73,8 @@ struct PrefillArgs {
     const int32_t* n_tiles_down;
     uint16_t* h16;           // [T*k, inter] bf16 by sorted position
     uint16_t* h_sh16;        // [T, shared_inter] bf16
-    float* o;                // [T*k, H]
-    float* o_sh;             // [T, H]
+    uint16_t* o16;           // [T*k, H] bf16 by sorted position (the reference's bf16 F.linear output)
+    uint16_t* o_sh16;        // [T, H] bf16
     int H, inter, sh_inter, E, k;
     int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
     int down_slabs;          // 256-row slabs per down workgroup

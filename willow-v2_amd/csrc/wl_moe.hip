@@ -483,13 +483,21 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
 
 // y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r]. For k <= 8
 // every index and weight of the token is loaded first and then every o row, so the loads overlap instead of forming
-// k dependent chains; the sum is the same in both forms.
+// k dependent chains; the sum is the same in both forms. OT: float (GEMV path) or uint16_t (bf16, MFMA path).
 constexpr int kCombineUnroll = 8;
 
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t* p) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__builtin_bit_cast(float, v.x << 16), __builtin_bit_cast(float, v.x & 0xFFFF0000u),
+                       __builtin_bit_cast(float, v.y << 16), __builtin_bit_cast(float, v.y & 0xFFFF0000u));
+}
+
+template <typename OT>
 __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int32_t* __restrict__ corder,
                                                  const int32_t* __restrict__ pair_pos,
-                                                 const float* __restrict__ wts, const float* __restrict__ o,
-                                                 const float* __restrict__ o_sh, const float* __restrict__ sg,
+                                                 const float* __restrict__ wts, const OT* __restrict__ o,
+                                                 const OT* __restrict__ o_sh, const float* __restrict__ sg,
                                                  float* __restrict__ y) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int h4 = H / 4;
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
             if (n < k && pos[n] >= 0 && pos[n] < P)  // never false for ids from k_topk; guards caller-supplied ids
-                ov[n] = *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos[n]) * H + r);
+                ov[n] = load4(o + static_cast<int64_t>(pos[n]) * H + r);
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
             if (n < k && pos[n] >= 0 && pos[n] < P) add(n, wv[n], ov[n]);
@@ -535,12 +543,12 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             const int64_t q = static_cast<int64_t>(t) * k + s;
             const int pos = pair_pos[q];
             if (pos < 0 || pos >= P) continue;
-            add(n, wts[q], *reinterpret_cast<const float4*>(o + static_cast<int64_t>(pos) * H + r));
+            add(n, wts[q], load4(o + static_cast<int64_t>(pos) * H + r));
         }
     }
     if (o_sh) {
         const float gv = sg ? sg[t] : 1.0f;
-        const float4 sv = *reinterpret_cast<const float4*>(o_sh + static_cast<int64_t>(t) * H + r);
+        const float4 sv = load4(o_sh + static_cast<int64_t>(t) * H + r);
         acc.x += gv * sv.x;
         acc.y += gv * sv.y;
         acc.z += gv * sv.z;
@@ -865,9 +873,14 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     }
     mark(5);
     const int64_t threads = tokens * (L.hidden / 4);
-    k_combine<<<static_cast<int>((threads + 255) / 256), 256, 0, s>>>(
-        static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos, w.wts, w.o, shared ? w.o_sh : nullptr,
-        sg, y);
+    const unsigned cgrid = static_cast<unsigned>((threads + 255) / 256);
+    if (mfma)
+        k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
+                                                  w.wts, reinterpret_cast<const uint16_t*>(w.o),
+                                                  shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg, y);
+    else
+        k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
+                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, y);
     rc = launch_status();
     mark(6);
     return rc;

@@ -615,7 +615,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
 }
 
 // down: a workgroup takes a.down_slabs consecutive 256-row slabs of the hidden dim (one pipeline across them); for
-// slab item, wavefront w has rows 256 (slab0 + item) + 16 kRT w + 16 r + lr. o fp32 by position. Its tiles hold at
+// slab item, wavefront w has rows 256 (slab0 + item) + 16 kRT w + 16 r + lr. o by position, rounded to bf16 as the
+// reference's bf16 F.linear output is (gguf/metal.py:407). Its tiles hold at
 // most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts within 256 registers).
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
@@ -636,7 +637,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
         return W + static_cast<int64_t>(row0 + 256 * item + 16 * r + lr) * rs;
     };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
-    float* out = sh ? a.o_sh : a.o;
+    uint16_t* out = sh ? a.o_sh16 : a.o16;
     auto epi = [&](int item, floatx4 (&acc)[kRT][kDownTileTokens / 16]) {
         const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -646,8 +647,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
                 const int t = 16 * n + lr;
                 if (t < count) {
                     const floatx4 v = acc[r][n];
-                    *reinterpret_cast<float4*>(out + static_cast<int64_t>(pos0 + t) * a.H + row0 + 256 * item +
-                                               16 * r + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * a.H + row0 + 256 * item +
+                                              16 * r + 4 * q) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
                 }
             }
         }
@@ -722,8 +723,8 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     a.n_tiles_down = w.n_tiles + 1;
     a.h16 = w.h16;
     a.h_sh16 = w.h_sh16;
-    a.o = w.o;
-    a.o_sh = w.o_sh;
+    a.o16 = reinterpret_cast<uint16_t*>(w.o);  // the fp32 buffers, half used
+    a.o_sh16 = reinterpret_cast<uint16_t*>(w.o_sh);
     a.H = L.hidden;
     a.inter = L.inter;
     a.sh_inter = shared ? L.shared_inter : 0;
