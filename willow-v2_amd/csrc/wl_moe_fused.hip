@@ -151,13 +151,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     };
 
     // workgroup b < H / kOwnRows owns output rows kOwnRows b .. + kOwnRows - 1; wavefront w < 8 / R takes rows
-    // kOwnRows b + R w + drow of the shared down matrix (fetched now, used once h_shared is known)
+    // kOwnRows b + R w + drow of the shared down matrix (fetched after phase A's loads, used once h_shared is known)
     const bool owner = b < H / kOwnRows;
     const bool sh_wave = wv < kOwnRows / R;
     RawLane<DN> shraw;
-    if (shared && sh_wave && owner)
-        shraw.fetch(a.sh_down + static_cast<int64_t>(kOwnRows * b + R * wv + drow) * dn_rs +
-                        kb * BlockInfo<DN>::bytes, c);
 
     // phase A: router rows, shared gate_up rows
     const int n_router = n_logits;  // one router row per wavefront task (lanes 0..31), more tasks in parallel
@@ -183,6 +180,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             if (lane == 0) put_tagged(a.sync, kTagHsh + 2 * j, tag, silu(g) * u);
         }
     }
+
+    // the shared down rows: requested only now, after phase A, whose router rows would otherwise queue behind them
+    if (shared && sh_wave && owner)
+        shraw.fetch(a.sh_down + static_cast<int64_t>(kOwnRows * b + R * wv + drow) * dn_rs +
+                        kb * BlockInfo<DN>::bytes, c);
 
     // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
     // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading.
