@@ -200,7 +200,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The candidates
     // (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are compacted
     // in LDS and each counts the candidates above it: up to 32 of them in one fixed pass over a zero-padded list.
-    // The k of rank < k place themselves; the weights follow wave_topk's arithmetic.
+    // The k of rank < k place themselves; their weights (wave_topk's arithmetic) are computed after the gate_up
+    // loads have been issued.
     static_assert(kFusedMaxK <= 8, "");
     if (wv == 0) {
         float v[EJ];
@@ -275,32 +276,15 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             if (lane + 64 * q < n_cand && above[q] < k)
                 lds_pick[above[q]] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck[q]));
         lane_sync();
-        // the max logit is pick 0's (softmax_stats' max, bitwise); the sum as softmax_sum adds it
+        // the picks in ascending id order for the tasks; the weights (needed only by the final sum) come later
         const int my_id = lane < k ? lds_pick[lane] : 0;
-        const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
-        const float m = lv0 == lv0 ? lv0 : -INFINITY;
-        float ssum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < EJ; j++)
-            if (valid[j]) ssum += expf(v[j] - m);
-        ssum = group_sum<64>(ssum);
-        const float lv = lds_logits[my_id];
-        const float my_w = pick_weight(lane < k ? (lv == lv ? lv : -INFINITY) : -INFINITY, m, ssum, k,
-                                       a.renorm != 0, lane);
         int idr[kFusedMaxK];
 #pragma unroll
         for (int q = 0; q < kFusedMaxK; q++) idr[q] = __builtin_amdgcn_readlane(my_id, q);
         int my_rank = 0;  // position among the k ids in ascending order
 #pragma unroll
         for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && idr[q] < my_id) ? 1 : 0;
-        if (lane < k) {
-            lds_sel[my_rank] = my_id;
-            lds_wsel[my_rank] = my_w;
-            if (b == 0) {
-                if (a.ids_out) a.ids_out[lane] = my_id;
-                if (a.wts_out) a.wts_out[lane] = my_w;
-            }
-        }
+        if (lane < k) lds_sel[my_rank] = my_id;
     }
     __syncthreads();
     int sel[kFusedMaxK];
@@ -325,6 +309,27 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const uint8_t* w = a.gate_up + static_cast<int64_t>(expert_of(s)) * a.gate_up_stride;
             graw[q][0].fetch(w + j * gu_rs + gi * BlockInfo<GU>::bytes, c);
             graw[q][1].fetch(w + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c);
+        }
+    }
+    // the routing weights, needed only by the final sum: wavefront 0 computes them while the loads above are in flight
+    // (softmax over all logits with the max from pick 0, as softmax_stats takes it; renormalised in pick order)
+    if (wv == 0) {
+        const int my_id = lane < k ? lds_pick[lane] : 0;
+        const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
+        const float m = lv0 == lv0 ? lv0 : -INFINITY;
+        const float ssum = softmax_sum<EJ>(lds_logits, E, lane, m);
+        const float lv = lds_logits[my_id];
+        const float my_w = pick_weight(lane < k ? (lv == lv ? lv : -INFINITY) : -INFINITY, m, ssum, k,
+                                       a.renorm != 0, lane);
+        int my_rank = 0;
+#pragma unroll
+        for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && __builtin_amdgcn_readlane(my_id, q) < my_id) ? 1 : 0;
+        if (lane < k) {
+            lds_wsel[my_rank] = my_w;
+            if (b == 0) {
+                if (a.ids_out) a.ids_out[lane] = my_id;
+                if (a.wts_out) a.wts_out[lane] = my_w;
+            }
         }
     }
     const int chunks_per_expert = H / kChunkRows;
