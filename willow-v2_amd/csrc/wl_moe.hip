@@ -100,6 +100,113 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
     }
 }
 
+// Small batches on the fp32 matrix core, the hidden dim split over the workgroup's wavefronts. A workgroup of 8
+// wavefronts computes one 16-token x 16-row tile (rows: experts, then the shared gate as row E); in round q,
+// wavefront w takes the 64-value segment 8 q + w: the 16 tokens' and 16 rows' values are staged in the wavefront's
+// own LDS area as [j][token or row][s] (20-float rows), and 16 v_mfma_f32_16x16x4_f32 from a zero accumulator give
+// the segment's partial for all 256 outputs, each a fused multiply-add chain in ascending k (the instruction's
+// four products are fused multiply-adds in k order, as k_router_mfma relies on). After each round, thread
+// (token, row) adds the round's partials to its running total in segment order. The next round's values are loaded
+// into registers while the current one is computed. With xb, the first row tile's workgroups also store the tokens'
+// values as bf16.
+constexpr bool kRouterSplit = true;  // k_router_split (else k_router) for small batches
+constexpr int kRsWaves = 8;
+constexpr int kRsRow = 20;                 // floats per staged (j, token) row: 16 values + 4 of padding
+constexpr int kRsTile = 4 * 16 * kRsRow;   // one staged operand
+
+__global__ __launch_bounds__(64 * kRsWaves) void k_router_split(const float* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ bias,
+                                                                const float* __restrict__ shared_gate, int T, int H,
+                                                                int E, float* __restrict__ logits,
+                                                                float* __restrict__ sg, uint16_t* __restrict__ xb) {
+    __shared__ __attribute__((aligned(16))) float stage[kRsWaves][2][kRsTile];
+    __shared__ float part[kRsWaves][16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+    const int rows = E + (shared_gate ? 1 : 0);
+    const int nseg = H / kRouterSeg;
+    // staging: float4 f = lane + 64 i (i < 4) holds values 4 (f % 16) .. + 3 of token / row f / 16
+    const float* xrow[4];
+    const float* wrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int f = lane + 64 * i, rr = f >> 4, c4 = 4 * (f & 15);
+        const int t = t0 + rr, r = r0 + rr;
+        xrow[i] = x + static_cast<int64_t>(t < T ? t : T - 1) * H + c4;
+        wrow[i] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + c4 : nullptr;
+    }
+    float4 xn[4], wn[4];
+    auto load = [&](int seg) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xn[i] = *reinterpret_cast<const float4*>(xrow[i] + seg * kRouterSeg);
+            wn[i] = wrow[i] ? *reinterpret_cast<const float4*>(wrow[i] + seg * kRouterSeg)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    float* sa = stage[wv][0];
+    float* sb = stage[wv][1];
+    const int lt = lane & 15, lj = lane >> 4;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    const int st = tid >> 4, sr = tid & 15;  // summing thread (tid < 256): token st, row sr
+    float total = 0.0f;
+    if (wv < nseg) load(wv);
+    for (int q0 = 0; q0 < nseg; q0 += kRsWaves) {
+        const int seg = q0 + wv;
+        if (seg < nseg) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int f = lane + 64 * i, rr = f >> 4, s4 = f & 15;
+                if (xb && blockIdx.y == 0 && t0 + rr < T)
+                    *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + seg * kRouterSeg + 4 * s4) =
+                        make_uint2(pack2(xn[i].x, xn[i].y), pack2(xn[i].z, xn[i].w));
+                sa[(0 * 16 + rr) * kRsRow + s4] = xn[i].x;
+                sa[(1 * 16 + rr) * kRsRow + s4] = xn[i].y;
+                sa[(2 * 16 + rr) * kRsRow + s4] = xn[i].z;
+                sa[(3 * 16 + rr) * kRsRow + s4] = xn[i].w;
+                sb[(0 * 16 + rr) * kRsRow + s4] = wn[i].x;
+                sb[(1 * 16 + rr) * kRsRow + s4] = wn[i].y;
+                sb[(2 * 16 + rr) * kRsRow + s4] = wn[i].z;
+                sb[(3 * 16 + rr) * kRsRow + s4] = wn[i].w;
+            }
+            if (seg + kRsWaves < nseg) load(seg + kRsWaves);
+            lane_sync();
+            floatx4 acc;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
+                const float4 av = *reinterpret_cast<const float4*>(&sa[(lj * 16 + lt) * kRsRow + 4 * q]);
+                const float4 bv = *reinterpret_cast<const float4*>(&sb[(lj * 16 + lt) * kRsRow + 4 * q]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, q == 0 ? zero : acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+            }
+            // lane holds D[4 lj + i][lt]: token 4 lj + i, row lt
+#pragma unroll
+            for (int i = 0; i < 4; i++) part[wv][4 * lj + i][lt] = acc[i];
+        }
+        __syncthreads();
+        if (tid < 256) {
+            const int n = min(kRsWaves, nseg - q0);
+            for (int u = 0; u < n; u++) {
+                const float v = part[u][st][sr];
+                total = (q0 == 0 && u == 0) ? v : __fadd_rn(total, v);
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < 256) {
+        const int t = t0 + st, r = r0 + sr;
+        if (t < T && r < rows) {
+            if (r < E)
+                logits[static_cast<int64_t>(t) * E + r] = bias ? __fadd_rn(total, bias[r]) : total;
+            else
+                sg[t] = sigmoid(total);
+        }
+    }
+}
+
 // One token: the shared router_row (the fused decode kernel computes the same rows with it).
 __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ x, const float* __restrict__ w,
                                                 const float* __restrict__ bias,
@@ -638,6 +745,10 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
     const int grid = (rows + 1) / 2;
     if (T == 1)
         k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
+    else if (kRouterSplit)
+        k_router_split<<<dim3(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>((rows + 15) / 16)),
+                          64 * kRsWaves, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T),
+                                                 L.hidden, L.n_experts, logits, sg, xb);
     else
         k_router<8><<<dim3(static_cast<unsigned>((rows + 15) / 16), static_cast<unsigned>((T + 7) / 8)), 256, 0, s>>>(
             x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg, xb);

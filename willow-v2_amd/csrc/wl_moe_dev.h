@@ -240,6 +240,7 @@ __device__ __forceinline__ void gate_up_row(const uint8_t* __restrict__ w, int j
 }
 
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Two floats -> two bf16 (round to nearest even, like Tensor.to(torch.bfloat16)) in one v_cvt_pk_bf16_f32.

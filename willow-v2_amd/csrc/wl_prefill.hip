@@ -25,7 +25,6 @@
 namespace wl {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 256;              // k per staged chunk: one K-quant block per row
 constexpr int kTileRowBytes = kBK * 2;                     // one token's chunk in LDS: 512 bytes, 32 slots of 16
