@@ -308,9 +308,12 @@ def main():
     log("stage us (b=1): " + ", ".join(f"{k} {v:.2f}" for k, v in stages.items()))
     U1 = sum(d1["unique"]) / len(d1["unique"])
     plan = layers[0].plan(1)
-    if plan == "fused":  # one kernel holds the whole layer; its events are stage 0's
-        dominant, dom_bytes, dom_us = "k_moe_decode", layer_bytes(1, U1), stages["router"]
-        stages = {"k_moe_decode": dom_us}
+    if plan == "fused":
+        # one kernel holds the whole layer, so the timed region is that kernel back to back: its events (on the
+        # stream the graphs replay on) over the launch count give the launch duration, gaps between launches
+        # included. The events around single eager launches also hold the launch latency.
+        dominant, dom_bytes, dom_us = "k_moe_decode", layer_bytes(1, U1), d1["us_per_layer"]
+        stages = {"k_moe_decode": dom_us, "k_moe_decode_eager_events": stages["router"]}
     else:  # the stage moving the most bytes
         dominant = max(("router", "gate_up", "down", "combine"), key=lambda n: stage_bytes(n, 1, U1))
         dom_bytes, dom_us = stage_bytes(dominant, 1, U1), stages[dominant]

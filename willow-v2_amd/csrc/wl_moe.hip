@@ -14,103 +14,18 @@ namespace wl {
 // Router. logits[t, e] = x[t] . W[e] (+ bias[e]) in a fixed order the CPU oracle replays exactly:
 //   k is cut into segments of kRouterSeg consecutive values; each segment's partial is a chain of fused
 //   multiply-adds in ascending k starting from 0; the partials are added left to right; then the bias.
-// Small batches (2 tokens up to the tiled kernel's minimum): a workgroup of 256 threads covers 16 rows x TT
-// tokens. The hidden dim is taken 16 segments at a time: the TT tokens' values of the chunk are staged in LDS with
-// coalesced loads (each 64-value segment padded to 68 floats, so that the 16 lanes reading 16 segments at once
-// spread over the banks), and lane (row 4 w + lane / 16, segment j = lane % 16) chains the TT tokens' partials of
-// segment 16 c + j from its row's 64 weights, loaded once. The partials go to LDS; thread (token u, row r) then
-// adds the chunk's partials to its output's running total, left to right. A ragged last token group recomputes its
-// last token for the missing ones and stores nothing for them. With xb, the first row group's workgroups also store
-// the tokens' values as bf16 (round to nearest even) while staging them, for the MFMA path.
 // The shared-expert gate is row E (weight vector shared_gate, no bias); its output is sigmoid(logit).
-constexpr int kRouterChunkSegs = 16;
-constexpr int kRouterPad = kRouterSeg + 4;
-
-template <int TT>
-__global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ w,
-                                                const float* __restrict__ bias,
-                                                const float* __restrict__ shared_gate, int T, int H, int E,
-                                                float* __restrict__ logits, float* __restrict__ sg,
-                                                uint16_t* __restrict__ xb) {
-    __shared__ __attribute__((aligned(16))) float xs[TT][kRouterChunkSegs * kRouterPad];
-    __shared__ float part[16 * TT][kRouterChunkSegs + 1];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int rl = 4 * (tid >> 6) + (lane >> 4), j = lane & 15;
-    const int row = blockIdx.x * 16 + rl;
-    const int rows_total = E + (shared_gate ? 1 : 0);
-    const float* wr = row < rows_total ? (row < E ? w + static_cast<int64_t>(row) * H : shared_gate) : w;
-    const int nseg = H / kRouterSeg;
-    const int t0 = blockIdx.y * TT;
-    // summing thread: token su, row sr
-    const int su = tid >> 4, sr = tid & 15;
-    float total = 0.0f;
-    for (int c = 0; c < nseg; c += kRouterChunkSegs) {
-        __syncthreads();  // the previous chunk's xs and part have been read
-#pragma unroll
-        for (int it = 0; it < TT; it++) {
-            const int f = tid + 256 * it;  // float4 f of the chunk: token f / 256, segment (f / 16) % 16, i = f % 16
-            const int u = f >> 8, sg4 = (f >> 4) & 15, i = f & 15;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (c + sg4 < nseg) {
-                const int64_t at = static_cast<int64_t>(min(t0 + u, T - 1)) * H + (c + sg4) * kRouterSeg + 4 * i;
-                v = *reinterpret_cast<const float4*>(x + at);
-                if (xb && blockIdx.x == 0 && t0 + u < T)
-                    *reinterpret_cast<uint2*>(xb + at) = make_uint2(pack2(v.x, v.y), pack2(v.z, v.w));
-            }
-            *reinterpret_cast<float4*>(&xs[u][sg4 * kRouterPad + 4 * i]) = v;
-        }
-        __syncthreads();
-        if (c + j < nseg) {
-            float p[TT];
-#pragma unroll
-            for (int u = 0; u < TT; u++) p[u] = 0.0f;
-            const float4* wp = reinterpret_cast<const float4*>(wr + (c + j) * kRouterSeg);
-#pragma unroll 4
-            for (int i = 0; i < kRouterSeg / 4; i++) {
-                const float4 wv = wp[i];
-#pragma unroll
-                for (int u = 0; u < TT; u++) {
-                    const float4 xv = *reinterpret_cast<const float4*>(&xs[u][j * kRouterPad + 4 * i]);
-                    p[u] = __builtin_fmaf(xv.x, wv.x, p[u]);
-                    p[u] = __builtin_fmaf(xv.y, wv.y, p[u]);
-                    p[u] = __builtin_fmaf(xv.z, wv.z, p[u]);
-                    p[u] = __builtin_fmaf(xv.w, wv.w, p[u]);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < TT; u++) part[rl * TT + u][j] = p[u];
-        }
-        __syncthreads();
-        if (tid < 16 * TT) {
-            const int n = min(kRouterChunkSegs, nseg - c);
-            for (int q = 0; q < n; q++) {
-                const float v = part[sr * TT + su][q];
-                total = (c == 0 && q == 0) ? v : __fadd_rn(total, v);
-            }
-        }
-    }
-    if (tid < 16 * TT) {
-        const int rr = blockIdx.x * 16 + sr, t = t0 + su;  // 16 consecutive rows of one token: contiguous stores
-        if (t < T && rr < rows_total) {
-            if (rr < E)
-                logits[static_cast<int64_t>(t) * E + rr] = bias ? __fadd_rn(total, bias[rr]) : total;
-            else
-                sg[t] = sigmoid(total);
-        }
-    }
-}
-
-// Small batches on the fp32 matrix core, the hidden dim split over the workgroup's wavefronts. A workgroup of 8
-// wavefronts computes one 16-token x 16-row tile (rows: experts, then the shared gate as row E); in round q,
-// wavefront w takes the 64-value segment 8 q + w: the 16 tokens' and 16 rows' values are staged in the wavefront's
-// own LDS area as [j][token or row][s] (20-float rows), and 16 v_mfma_f32_16x16x4_f32 from a zero accumulator give
-// the segment's partial for all 256 outputs, each a fused multiply-add chain in ascending k (the instruction's
-// four products are fused multiply-adds in k order, as k_router_mfma relies on). After each round, thread
-// (token, row) adds the round's partials to its running total in segment order. The next round's values are loaded
-// into registers while the current one is computed. With xb, the first row tile's workgroups also store the tokens'
-// values as bf16.
-constexpr bool kRouterSplit = true;  // k_router_split (else k_router) for small batches
+// Small batches (2 tokens up to the tiled kernel's minimum) on the fp32 matrix core, the hidden dim split over the
+// workgroup's wavefronts. A workgroup of 8 wavefronts computes one 16-token x 16-row tile (rows: experts, then the
+// shared gate as row E). The 64-value segments are taken in rounds of 8 kRsDepth: wavefront w first loads segments
+// 8 d + w (d < kRsDepth) of the round into registers, all at once, then for each d stages the 16 tokens' and 16 rows'
+// values of its segment in its own LDS area as [j][token or row][s] (20-float rows) and runs 16 v_mfma_f32_16x16x4_f32
+// from a zero accumulator: the segment's partial for all 256 outputs, each a fused multiply-add chain in ascending k
+// (the instruction's four products are fused multiply-adds in k order, as k_router_mfma relies on). After the round,
+// thread (token, row) adds the round's partials to its running total in segment order. With xb, the first row tile's
+// workgroups also store the tokens' values as bf16.
 constexpr int kRsWaves = 8;
+constexpr int kRsDepth = 4;                // segments per wavefront held in registers
 constexpr int kRsRow = 20;                 // floats per staged (j, token) row: 16 values + 4 of padding
 constexpr int kRsTile = 4 * 16 * kRsRow;   // one staged operand
 
@@ -121,7 +36,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_router_split(const float* __r
                                                                 int E, float* __restrict__ logits,
                                                                 float* __restrict__ sg, uint16_t* __restrict__ xb) {
     __shared__ __attribute__((aligned(16))) float stage[kRsWaves][2][kRsTile];
-    __shared__ float part[kRsWaves][16][17];
+    __shared__ float part[kRsDepth * kRsWaves][16][17];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
     const int rows = E + (shared_gate ? 1 : 0);
@@ -136,59 +51,66 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_router_split(const float* __r
         xrow[i] = x + static_cast<int64_t>(t < T ? t : T - 1) * H + c4;
         wrow[i] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + c4 : nullptr;
     }
-    float4 xn[4], wn[4];
-    auto load = [&](int seg) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            xn[i] = *reinterpret_cast<const float4*>(xrow[i] + seg * kRouterSeg);
-            wn[i] = wrow[i] ? *reinterpret_cast<const float4*>(wrow[i] + seg * kRouterSeg)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
     float* sa = stage[wv][0];
     float* sb = stage[wv][1];
     const int lt = lane & 15, lj = lane >> 4;
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     const int st = tid >> 4, sr = tid & 15;  // summing thread (tid < 256): token st, row sr
     float total = 0.0f;
-    if (wv < nseg) load(wv);
-    for (int q0 = 0; q0 < nseg; q0 += kRsWaves) {
-        const int seg = q0 + wv;
-        if (seg < nseg) {
+    for (int q0 = 0; q0 < nseg; q0 += kRsWaves * kRsDepth) {
+        float4 xn[kRsDepth][4], wn[kRsDepth][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int f = lane + 64 * i, rr = f >> 4, s4 = f & 15;
-                if (xb && blockIdx.y == 0 && t0 + rr < T)
-                    *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + seg * kRouterSeg + 4 * s4) =
-                        make_uint2(pack2(xn[i].x, xn[i].y), pack2(xn[i].z, xn[i].w));
-                sa[(0 * 16 + rr) * kRsRow + s4] = xn[i].x;
-                sa[(1 * 16 + rr) * kRsRow + s4] = xn[i].y;
-                sa[(2 * 16 + rr) * kRsRow + s4] = xn[i].z;
-                sa[(3 * 16 + rr) * kRsRow + s4] = xn[i].w;
-                sb[(0 * 16 + rr) * kRsRow + s4] = wn[i].x;
-                sb[(1 * 16 + rr) * kRsRow + s4] = wn[i].y;
-                sb[(2 * 16 + rr) * kRsRow + s4] = wn[i].z;
-                sb[(3 * 16 + rr) * kRsRow + s4] = wn[i].w;
+        for (int d = 0; d < kRsDepth; d++) {
+            const int seg = q0 + kRsWaves * d + wv;
+            if (seg < nseg) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    xn[d][i] = *reinterpret_cast<const float4*>(xrow[i] + seg * kRouterSeg);
+                    wn[d][i] = wrow[i] ? *reinterpret_cast<const float4*>(wrow[i] + seg * kRouterSeg)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
-            if (seg + kRsWaves < nseg) load(seg + kRsWaves);
-            lane_sync();
-            floatx4 acc;
+        }
 #pragma unroll
-            for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
-                const float4 av = *reinterpret_cast<const float4*>(&sa[(lj * 16 + lt) * kRsRow + 4 * q]);
-                const float4 bv = *reinterpret_cast<const float4*>(&sb[(lj * 16 + lt) * kRsRow + 4 * q]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, q == 0 ? zero : acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+        for (int d = 0; d < kRsDepth; d++) {
+            const int seg = q0 + kRsWaves * d + wv;
+            if (seg < nseg) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int f = lane + 64 * i, rr = f >> 4, s4 = f & 15;
+                    const float4 xv = xn[d][i], wv4 = wn[d][i];
+                    if (xb && blockIdx.y == 0 && t0 + rr < T)
+                        *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + seg * kRouterSeg +
+                                                  4 * s4) = make_uint2(pack2(xv.x, xv.y), pack2(xv.z, xv.w));
+                    sa[(0 * 16 + rr) * kRsRow + s4] = xv.x;
+                    sa[(1 * 16 + rr) * kRsRow + s4] = xv.y;
+                    sa[(2 * 16 + rr) * kRsRow + s4] = xv.z;
+                    sa[(3 * 16 + rr) * kRsRow + s4] = xv.w;
+                    sb[(0 * 16 + rr) * kRsRow + s4] = wv4.x;
+                    sb[(1 * 16 + rr) * kRsRow + s4] = wv4.y;
+                    sb[(2 * 16 + rr) * kRsRow + s4] = wv4.z;
+                    sb[(3 * 16 + rr) * kRsRow + s4] = wv4.w;
+                }
+                lane_sync();
+                floatx4 acc;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
+                    const float4 av = *reinterpret_cast<const float4*>(&sa[(lj * 16 + lt) * kRsRow + 4 * q]);
+                    const float4 bv = *reinterpret_cast<const float4*>(&sb[(lj * 16 + lt) * kRsRow + 4 * q]);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, q == 0 ? zero : acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+                }
+                // lane holds D[4 lj + i][lt]: token 4 lj + i, row lt
+#pragma unroll
+                for (int i = 0; i < 4; i++) part[kRsWaves * d + wv][4 * lj + i][lt] = acc[i];
+                lane_sync();  // the staging area is rewritten for the next d
             }
-            // lane holds D[4 lj + i][lt]: token 4 lj + i, row lt
-#pragma unroll
-            for (int i = 0; i < 4; i++) part[wv][4 * lj + i][lt] = acc[i];
         }
         __syncthreads();
         if (tid < 256) {
-            const int n = min(kRsWaves, nseg - q0);
+            const int n = min(kRsWaves * kRsDepth, nseg - q0);
             for (int u = 0; u < n; u++) {
                 const float v = part[u][st][sr];
                 total = (q0 == 0 && u == 0) ? v : __fadd_rn(total, v);
@@ -745,13 +667,10 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
     const int grid = (rows + 1) / 2;
     if (T == 1)
         k_router1<<<grid, 64, 0, s>>>(x, L.router, L.router_bias, shared_gate, L.hidden, L.n_experts, logits, sg);
-    else if (kRouterSplit)
+    else
         k_router_split<<<dim3(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>((rows + 15) / 16)),
                           64 * kRsWaves, 0, s>>>(x, L.router, L.router_bias, shared_gate, static_cast<int>(T),
                                                  L.hidden, L.n_experts, logits, sg, xb);
-    else
-        k_router<8><<<dim3(static_cast<unsigned>((rows + 15) / 16), static_cast<unsigned>((T + 7) / 8)), 256, 0, s>>>(
-            x, L.router, L.router_bias, shared_gate, static_cast<int>(T), L.hidden, L.n_experts, logits, sg, xb);
     return launch_status();
 }
 
