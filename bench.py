@@ -8,8 +8,9 @@ change (and the 256 MB Infinity Cache cannot serve repeats). One step = one toke
 once as a HIP graph per input set and replayed.
   value = microseconds per token per layer (lower is better); hbm_gbps = algorithmic bytes / that time.
 Also reported (same JSON line): batched decode at 64 tokens with Zipf(1.1)-shaped routing, and a 4096-token
-prefill chunk, each through the 40 layers; the per-stage kernel times of the layer (HIP events, live); and the CPU
-oracle (numpy dequantize + fp32 matmul) timed on a bounded sample on this host.
+prefill chunk, each through the 40 layers; the per-stage kernel times of the layer (HIP events, live); the rate
+of loading a synthetic GGUF file's experts into HBM (gguf.loader); and the CPU oracle (numpy dequantize + fp32
+matmul) timed on a bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -272,6 +273,9 @@ def main():
     ap.add_argument("--skip-b64", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-load", action="store_true")
+    ap.add_argument("--load-layers", type=int, default=2,
+                    help="full-shape layers in the synthetic GGUF file of the loader measurement")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode layers eagerly instead of replaying HIP graphs (for counter runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -352,6 +356,8 @@ def main():
                                 "mean_unique_experts": round(sum(d64["unique"]) / len(d64["unique"]), 1),
                                 "routing": "Zipf(1.1) router bias"}
         del d64
+    if not args.skip_load:
+        result["gguf_load"] = run_gguf_load(torch, args.load_layers)
     if not args.skip_cpu:
         log("timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline()
@@ -380,6 +386,71 @@ def run_prefill(torch, hip, layers, T, steps):
             "tflops": round(flops / ms / 1e9, 2), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
             "path": layers[0].plan(T) + ": tiled fp32 router, bf16 MFMA grouped expert GEMMs (in-register "
                     "Q4_K/Q6_K dequant), fp32 combine"}
+
+
+def run_gguf_load(torch, n_layers):
+    """GGUF file -> HBM: a synthetic Qwen3.6-shaped GGUF of n_layers MoE layers (random block bytes; the loader
+    does not look at them) is written to a temporary directory and loaded with gguf.loader.load_experts. The file
+    was just written, so it is read from the page cache: the figure is the loader's host-to-HBM rate, compared with
+    a plain pinned host-to-device copy of 256 MiB timed the same way."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    from gguf import loader
+    from gguf.writer import write_gguf
+
+    rng = np.random.default_rng(9)
+    arch = "qwen35moe"
+    meta = {"general.architecture": arch, f"{arch}.block_count": n_layers, f"{arch}.embedding_length": HIDDEN,
+            f"{arch}.expert_count": EXPERTS, f"{arch}.expert_used_count": TOP_K}
+    tensors, want = [], []
+    for n in range(n_layers):
+        gate = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
+        up = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
+        down = rng.integers(0, 256, (EXPERTS, DOWN_BYTES), dtype=np.uint8)
+        tensors += [(f"blk.{n}.ffn_gate_exps.weight", "Q4_K", (EXPERTS, INTER, HIDDEN), gate),
+                    (f"blk.{n}.ffn_up_exps.weight", "Q4_K", (EXPERTS, INTER, HIDDEN), up),
+                    (f"blk.{n}.ffn_down_exps.weight", "Q6_K", (EXPERTS, HIDDEN, INTER), down)]
+        want.append((gate, up, down))
+    folder = tempfile.mkdtemp(prefix="wl_gguf_")
+    try:
+        path = os.path.join(folder, "synthetic-moe.gguf")
+        write_gguf(path, meta, tensors)
+        del tensors
+        header = loader.read_gguf(path)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        store = loader.load_experts(header, "cuda")
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        # spot check: first, middle and last expert of every layer, byte for byte
+        for n, (gate, up, down) in enumerate(want):
+            l = store.layers[n]
+            for e in (0, EXPERTS // 2, EXPERTS - 1):
+                gu = l.gate_up[e].cpu().numpy()
+                half = GATE_UP_BYTES // 2
+                assert np.array_equal(gu[:half], gate[e]) and np.array_equal(gu[half:], up[e])
+                assert np.array_equal(l.down[e].cpu().numpy(), down[e])
+        nbytes = store.loaded_bytes
+        del store
+    finally:
+        shutil.rmtree(folder, ignore_errors=True)
+    host = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    dev = torch.empty_like(host, device="cuda")
+    dev.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(4):
+        dev.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    copy_gbps = 4 * host.numel() / (time.perf_counter() - t0) / 1e9
+    gbps = nbytes / dt / 1e9
+    log(f"GGUF -> HBM: {nbytes / 1e9:.2f} GB of experts ({n_layers} layers) in {dt:.2f} s, {gbps:.1f} GB/s "
+        f"(pinned copy {copy_gbps:.1f} GB/s)")
+    return {"layers": n_layers, "bytes": nbytes, "seconds": round(dt, 3), "gbps": round(gbps, 2),
+            "pinned_copy_gbps": round(copy_gbps, 2), "frac_of_pinned_copy": round(gbps / copy_gbps, 3),
+            "source": "page cache (file just written)"}
 
 
 if __name__ == "__main__":

@@ -114,3 +114,34 @@ def moe_layer(seed: int, hidden: int = 2048, inter: int = 512, shared_inter: int
 def tokens(seed: int, count: int, hidden: int = 2048) -> np.ndarray:
     """x ~ N(0,1) fp32 [count, hidden] from its own generator."""
     return np.random.default_rng(seed).standard_normal((count, hidden)).astype(np.float32)
+
+
+def write_moe_gguf(path: str, layers: list, arch: str = "qwen35moe", extra_metadata: dict = None,
+                   alignment: int = 32):
+    """A GGUF file holding the MoE blocks of `layers` (moe_layer dicts; every layer the same shape) under
+    llama.cpp's tensor names: blk.N.ffn_{gate,up,down}_exps.weight stacked [experts, out, in], ffn_gate_inp.weight
+    (router, F32 [experts, hidden]), ffn_gate_inp_shexp.weight (F32 [hidden]) and ffn_{gate,up,down}_shexp.weight,
+    with the metadata keys the loader reads. Layers may differ in down type."""
+    from .writer import write_gguf
+
+    lw0 = layers[0]
+    H, I, SI, E = lw0["hidden"], lw0["inter"], lw0["shared_inter"], lw0["experts"]
+    metadata = {"general.architecture": arch, "general.alignment": alignment, f"{arch}.block_count": len(layers),
+                f"{arch}.embedding_length": H, f"{arch}.expert_count": E, f"{arch}.expert_used_count": lw0["top_k"],
+                f"{arch}.expert_feed_forward_length": I, f"{arch}.expert_shared_feed_forward_length": SI}
+    metadata.update(extra_metadata or {})
+    tensors = []
+    for n, lw in enumerate(layers):
+        gu, dt = lw["gate_up_type"], lw["down_type"]
+        p = f"blk.{n}."
+        tensors += [
+            (p + "ffn_gate_inp.weight", "F32", (E, H), lw["router"]),
+            (p + "ffn_gate_exps.weight", gu, (E, I, H), np.ascontiguousarray(lw["gate_up"][:, :I])),
+            (p + "ffn_up_exps.weight", gu, (E, I, H), np.ascontiguousarray(lw["gate_up"][:, I:])),
+            (p + "ffn_down_exps.weight", dt, (E, H, I), lw["down"]),
+            (p + "ffn_gate_inp_shexp.weight", "F32", (H,), lw["shared_gate"]),
+            (p + "ffn_gate_shexp.weight", lw["shared_gate_up_type"], (SI, H), lw["shared_gate_up"][:SI]),
+            (p + "ffn_up_shexp.weight", lw["shared_gate_up_type"], (SI, H), lw["shared_gate_up"][SI:]),
+            (p + "ffn_down_shexp.weight", lw["shared_down_type"], (H, SI), lw["shared_down"]),
+        ]
+    write_gguf(path, metadata, tensors, alignment=alignment)
