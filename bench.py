@@ -274,7 +274,7 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-load", action="store_true")
-    ap.add_argument("--load-layers", type=int, default=2,
+    ap.add_argument("--load-layers", type=int, default=8,
                     help="full-shape layers in the synthetic GGUF file of the loader measurement")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode layers eagerly instead of replaying HIP graphs (for counter runs)")
@@ -404,15 +404,15 @@ def run_gguf_load(torch, n_layers):
     arch = "qwen35moe"
     meta = {"general.architecture": arch, f"{arch}.block_count": n_layers, f"{arch}.embedding_length": HIDDEN,
             f"{arch}.expert_count": EXPERTS, f"{arch}.expert_used_count": TOP_K}
-    tensors, want = [], []
+    # one layer's random bytes, written for every layer (the content does not matter to the loader)
+    gate = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
+    up = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
+    down = rng.integers(0, 256, (EXPERTS, DOWN_BYTES), dtype=np.uint8)
+    tensors = []
     for n in range(n_layers):
-        gate = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
-        up = rng.integers(0, 256, (EXPERTS, GATE_UP_BYTES // 2), dtype=np.uint8)
-        down = rng.integers(0, 256, (EXPERTS, DOWN_BYTES), dtype=np.uint8)
         tensors += [(f"blk.{n}.ffn_gate_exps.weight", "Q4_K", (EXPERTS, INTER, HIDDEN), gate),
                     (f"blk.{n}.ffn_up_exps.weight", "Q4_K", (EXPERTS, INTER, HIDDEN), up),
                     (f"blk.{n}.ffn_down_exps.weight", "Q6_K", (EXPERTS, HIDDEN, INTER), down)]
-        want.append((gate, up, down))
     folder = tempfile.mkdtemp(prefix="wl_gguf_")
     try:
         path = os.path.join(folder, "synthetic-moe.gguf")
@@ -425,8 +425,7 @@ def run_gguf_load(torch, n_layers):
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         # spot check: first, middle and last expert of every layer, byte for byte
-        for n, (gate, up, down) in enumerate(want):
-            l = store.layers[n]
+        for l in store.layers:
             for e in (0, EXPERTS // 2, EXPERTS - 1):
                 gu = l.gate_up[e].cpu().numpy()
                 half = GATE_UP_BYTES // 2

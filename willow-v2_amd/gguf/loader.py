@@ -9,8 +9,8 @@ shared-expert gate, shared expert) are loaded under the Hugging Face names Engin
 (engines/qwen36/loader.py:37-41), the shared expert's quantized matrices as GGMLWeight views that stay quantized on
 the GPU. Each layer keeps its own down type (Q4_K_M mixes Q6_K and Q4_K down layers, gguf/compiler.py:42-44).
 
-File bytes are read with preadv into pinned staging buffers and copied to the device asynchronously, two buffers
-in flight, so reading the file overlaps the host-to-device copies.
+File bytes are read with preadv by several threads into a ring of pinned staging buffers and copied to the device
+asynchronously, so reading the file overlaps the host-to-device copies.
 """
 import os
 
@@ -55,15 +55,18 @@ def moe_config(model) -> dict:
 
 
 class _Stager:
-    """File ranges -> device tensors through two pinned buffers of `chunk` bytes."""
+    """File ranges -> device tensors through `depth` pinned buffers of `chunk` bytes: `threads` reader threads
+    fill buffers with preadv (which runs without the GIL) while the main thread issues the host-to-device copies of
+    the buffers already read, in order. A buffer is read into again only after its last copy has completed."""
 
-    def __init__(self, device, chunk: int):
+    def __init__(self, device, chunk: int, depth: int = 8, threads: int = 8):
         self.device = torch.device(device)
         self.chunk = chunk
-        self.bufs = [torch.empty(chunk, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self.bufs = [torch.empty(chunk, dtype=torch.uint8, pin_memory=True) for _ in range(depth)]
         self.views = [memoryview(b.numpy()) for b in self.bufs]
-        self.events = [None, None]
-        self.turn = 0
+        self.events = [None] * depth
+        self.threads = threads
+        self.jobs = []
         self.fds = {}
         self.bytes = 0
 
@@ -72,28 +75,70 @@ class _Stager:
             self.fds[path] = os.open(path, os.O_RDONLY)
         return self.fds[path]
 
-    def copy(self, path: str, offset: int, dst: torch.Tensor, row_bytes: int):
-        """dst ([n, row_bytes] uint8 device view, rows may be strided) <- the n * row_bytes bytes at offset."""
-        n = dst.shape[0]
-        per = max(1, self.chunk // row_bytes)
-        if row_bytes > self.chunk:
-            raise ValueError(f"a {row_bytes}-byte row does not fit the {self.chunk}-byte staging buffer")
-        fd = self._fd(path)
+    def add(self, dst: torch.Tensor, sources: list):
+        """Queue dst ([n, W] contiguous uint8 device tensor) <- row i = the concatenation of the file ranges
+        sources[i] = [(path, offset, size), ...] (sizes summing to W). Rows are staged a chunk of whole rows at a
+        time; within a chunk, each column piece is read with one preadv per run of rows whose ranges lie back to
+        back in the file, scattered straight into the rows' places in the staging buffer."""
+        n, width = dst.shape
+        if width > self.chunk:
+            raise ValueError(f"a {width}-byte row does not fit the {self.chunk}-byte staging buffer")
+        if sum(size for _, _, size in sources[0]) != width:
+            raise ValueError(f"the pieces of a row do not add up to its {width} bytes")
+        per = min(self.chunk // width, 512)  # 512 rows: within the kernel's limit on preadv buffers (IOV_MAX)
         for r0 in range(0, n, per):
             r1 = min(n, r0 + per)
-            nbytes = (r1 - r0) * row_bytes
-            i = self.turn
-            self.turn ^= 1
-            if self.events[i] is not None:
-                self.events[i].synchronize()  # the buffer's previous copy has left it
-            got = os.preadv(fd, [self.views[i][:nbytes]], offset + r0 * row_bytes)
+            reads, col = [], 0
+            for j, (_, _, size) in enumerate(sources[r0]):
+                run = None
+                for r in range(r0, r1):
+                    path, offset, sz = sources[r][j]
+                    if sz != size:
+                        raise ValueError(f"row {r} piece {j} has {sz} bytes, row {r0} has {size}")
+                    if run is not None and run[1] == path and run[2] + run[3] == offset:
+                        run[3] += size
+                        run[4].append((r - r0) * width + col)
+                    else:
+                        run = [self._fd(path), path, offset, size, [(r - r0) * width + col]]
+                        reads.append(run)
+                col += size
+            self.jobs.append((reads, dst[r0:r1]))
+
+    def _read(self, slot, reads):
+        view = self.views[slot]
+        for fd, path, offset, nbytes, places in reads:
+            size = nbytes // len(places)
+            got = os.preadv(fd, [view[p:p + size] for p in places], offset)
             if got != nbytes:
-                raise IOError(f"short read in {path}: {got} of {nbytes} bytes at {offset + r0 * row_bytes}")
-            dst[r0:r1].copy_(self.bufs[i][:nbytes].view(r1 - r0, row_bytes), non_blocking=True)
+                raise IOError(f"short read in {path}: {got} of {nbytes} bytes at {offset}")
+
+    def run(self):
+        from collections import deque
+        from concurrent.futures import ThreadPoolExecutor
+
+        depth = len(self.bufs)
+        pending = deque()
+
+        def finish():
+            slot, fut, dst = pending.popleft()
+            fut.result()
+            dst.copy_(self.bufs[slot][:dst.numel()].view(dst.shape), non_blocking=True)
             ev = torch.cuda.Event()
             ev.record()
-            self.events[i] = ev
-            self.bytes += nbytes
+            self.events[slot] = ev
+            self.bytes += dst.numel()
+
+        with ThreadPoolExecutor(self.threads) as pool:
+            for i, (reads, dst) in enumerate(self.jobs):
+                slot = i % depth
+                if len(pending) == depth:
+                    finish()
+                if self.events[slot] is not None:
+                    self.events[slot].synchronize()  # the slot's previous copy has left it
+                pending.append((slot, pool.submit(self._read, slot, reads), dst))
+            while pending:
+                finish()
+        self.jobs = []
 
     def close(self):
         for ev in self.events:
@@ -104,28 +149,13 @@ class _Stager:
         self.fds = {}
 
 
-def _runs(sources_by_expert, part_index):
-    """Split experts 0..E-1 into runs whose part_index source ranges are back to back in one file:
-    [(e0, e1, path, offset, size)]. A stacked ffn_*_exps tensor is one run."""
-    runs = []
-    for e, sources in enumerate(sources_by_expert):
-        path, offset, size = sources[part_index]
-        if runs:
-            e0, e1, p, o, s = runs[-1]
-            if p == path and s == size and e == e1 and offset == o + (e1 - e0) * s:
-                runs[-1] = (e0, e + 1, p, o, s)
-                continue
-        runs.append((e, e + 1, path, offset, size))
-    return runs
-
-
-def load_experts(model, device="cuda", chunk_bytes: int = 64 << 20) -> HBMExpertStore:
+def load_experts(model, device="cuda", chunk_bytes: int = 32 << 20, threads: int = 8) -> HBMExpertStore:
     """Every layer's routed experts in HBM: an HBMExpertStore whose layer l holds gate_up [E, gate rows then up
     rows] and down [E, rows] exactly as the file's blocks (gate and up fused per expert as fuse_gate_up plans it)."""
     metadata, tensors = _header(model)
     num_layers, num_experts, _, plan, part_info = scan_experts(metadata, tensors)
     plan, part_info = fuse_gate_up(plan, part_info)
-    stager = _Stager(device, chunk_bytes)
+    stager = _Stager(device, chunk_bytes, threads=threads)
     layers = []
     try:
         for layer in range(num_layers):
@@ -141,19 +171,14 @@ def load_experts(model, device="cuda", chunk_bytes: int = 64 << 20) -> HBMExpert
             dn_bytes = dn_src[0][0][2]
             gate_up = torch.empty(num_experts, gu_bytes, dtype=torch.uint8, device=device)
             down = torch.empty(num_experts, dn_bytes, dtype=torch.uint8, device=device)
-            col = 0
-            for j in range(len(gu_src[0])):  # gate, then up (or the one fused source)
-                width = gu_src[0][j][2]
-                for e0, e1, path, offset, size in _runs(gu_src, j):
-                    stager.copy(path, offset, gate_up[e0:e1, col:col + width], size)
-                col += width
-            for e0, e1, path, offset, size in _runs(dn_src, 0):
-                stager.copy(path, offset, down[e0:e1], size)
+            stager.add(gate_up, gu_src)  # gate rows then up rows (or the one fused source)
+            stager.add(down, dn_src)
             inter, hidden = gu["shape"][0] // 2, gu["shape"][1]
             if dn["shape"] != [hidden, inter]:
                 raise ValueError(f"layer {layer}: down has shape {dn['shape']}, expected {[hidden, inter]}")
             layers.append(LayerExperts(gate_up=gate_up, down=down, gate_up_type=gu["dtype"], down_type=dn["dtype"],
                                        hidden=hidden, inter=inter))
+        stager.run()
     finally:
         stager.close()
     store = HBMExpertStore(layers, device)
