@@ -428,16 +428,17 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
 }
 
-template <int TILE>
+template <int TILE, int NT>
 __device__ __forceinline__ void stage_async(uint32_t buf, const uint8_t* src, const uint32_t* rowtab, uint32_t col,
                                             int wv, int half) {
     constexpr int kIters = stage_iters<TILE>();
+    static_assert(NT <= kIters, "");
     const uint32_t* tab = rowtab + kIters * (2 * wv + half);
-    uint32_t off[kIters];
+    uint32_t off[NT];
 #pragma unroll
-    for (int i = 0; i < kIters; i++) off[i] = tab[i];
+    for (int i = 0; i < NT; i++) off[i] = tab[i];
 #pragma unroll
-    for (int it = 0; it < kIters; it++) {
+    for (int it = 0; it < NT; it++) {  // iteration it: tokens 16 it .. 16 it + 15, token tile it
         // M0 (the LDS destination) is a register the compiler reserves: saved and restored around the load
         uint32_t saved;
         asm volatile(
@@ -478,7 +479,7 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     RowState<TYPE> rs[kRT], nx[kRT];
 #pragma unroll
     for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(0, r, lr), q);
-    stage_async<TILE>(lds0, src, rowtab, col, wv, half);
+    stage_async<TILE, NT>(lds0, src, rowtab, col, wv, half);
     bf16x8 a0[kRT], a1[kRT], b[NT];
     const int nsteps = nitems * nblocks;
     for (int st = 0; st < nsteps; st++) {
@@ -491,7 +492,7 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
             nx[r].fetch(row_ptr(in, r, lr) + static_cast<int64_t>(kn) * BlockInfo<TYPE>::bytes, q);
         const bool resident = nblocks <= 2;
         if (st + 1 < nsteps && (!resident || sn < nblocks))
-            stage_async<TILE>((resident ? kn : ((st + 1) & 1)) ? lds1 : lds0,
+            stage_async<TILE, NT>((resident ? kn : ((st + 1) & 1)) ? lds1 : lds0,
                               src + static_cast<int64_t>(kn) * kTileRowBytes, rowtab, col, wv, half);
         const uint8_t* buf = bufs[resident ? st - (st / nblocks) * nblocks : (st & 1)];
         read_b<TYPE, NT, 0>(buf, ba, b);
@@ -527,9 +528,9 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
 // ---------------------------------------------------------------------------------------------------------------
 // The GEMM core: a workgroup of kGemmWaves wavefronts, each owning kRT row tiles of 16 (rows given by
 // row_ptr(item, r, lr), for nitems row sets one after another) and the tile's up to TILE tokens as NT token tiles of
-// 16 (NT = TILE / 16, 8 or 4, the fewest that cover `count`). Per K chunk of 256 values (one block per row) the
-// activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes kRT A-fragments and runs
-// kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in src ([*, ld] bf16);
+// 16 (NT = TILE / 16, 8, 4 or 1, the fewest that cover `count`; only those are staged). Per K chunk of 256 values
+// (one block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes kRT
+// A-fragments and runs kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in src ([*, ld] bf16);
 // rows past count load token 0's (their results are never stored).
 template <int TYPE, int TILE, typename RowPtr, typename SrcRow, typename Epilogue>
 __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][TILE / 16],
@@ -550,8 +551,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()]
         gemm_loop<TYPE, TILE, NTA, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
     else if (count > 64)
         gemm_loop<TYPE, TILE, 8, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
-    else
+    else if (count > 16)
         gemm_loop<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
+    else
+        gemm_loop<TYPE, TILE, 1, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its own L2. slab_tile maps the linear
