@@ -510,16 +510,27 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
     }
 }
 
-// y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r]. For k <= 8
-// every index and weight of the token is loaded first and then every o row, so the loads overlap instead of forming
-// k dependent chains; the sum is the same in both forms. OT: float (GEMV path) or uint16_t (bf16, MFMA path).
+// y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r]. A workgroup
+// takes kCombineSpan values of one token, 8 per thread, so the token's routing (indices and weights, the same for
+// the whole workgroup) is read with scalar loads once per workgroup. For k <= 8 every index and weight is loaded
+// first and then every o row, so the loads overlap instead of forming k dependent chains; the sum is the same in
+// both forms. OT: float (GEMV path) or uint16_t (bf16, MFMA path). H is a multiple of 8.
 constexpr int kCombineUnroll = 8;
+constexpr int kCombineSpan = 8 * 256;
 
-__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ __forceinline__ float4 load4(const uint16_t* p) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    return make_float4(__builtin_bit_cast(float, v.x << 16), __builtin_bit_cast(float, v.x & 0xFFFF0000u),
-                       __builtin_bit_cast(float, v.y << 16), __builtin_bit_cast(float, v.y & 0xFFFF0000u));
+struct Float8 {
+    float4 a, b;
+};
+__device__ __forceinline__ Float8 load8(const float* p) {
+    return {*reinterpret_cast<const float4*>(p), *reinterpret_cast<const float4*>(p + 4)};
+}
+__device__ __forceinline__ float4 bf16x4_to_float4(uint32_t lo, uint32_t hi) {
+    return make_float4(__builtin_bit_cast(float, lo << 16), __builtin_bit_cast(float, lo & 0xFFFF0000u),
+                       __builtin_bit_cast(float, hi << 16), __builtin_bit_cast(float, hi & 0xFFFF0000u));
+}
+__device__ __forceinline__ Float8 load8(const uint16_t* p) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    return {bf16x4_to_float4(v.x, v.y), bf16x4_to_float4(v.z, v.w)};
 }
 
 template <typename OT>
@@ -528,21 +539,26 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
                                                  const float* __restrict__ wts, const OT* __restrict__ o,
                                                  const OT* __restrict__ o_sh, const float* __restrict__ sg,
                                                  float* __restrict__ y) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int h4 = H / 4;
-    if (i >= static_cast<int64_t>(T) * h4) return;
-    const int t = static_cast<int>(i / h4);
-    const int r = static_cast<int>(i - static_cast<int64_t>(t) * h4) * 4;
+    const int spans = (H + kCombineSpan - 1) / kCombineSpan;
+    const int t = static_cast<int>(blockIdx.x) / spans;
+    const int r = (static_cast<int>(blockIdx.x) - t * spans) * kCombineSpan + 8 * static_cast<int>(threadIdx.x);
+    if (t >= T || r >= H) return;
     const int P = T * k;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto add = [&](int n, float wv, float4 ov) {
+    const int64_t base = static_cast<int64_t>(t) * k;
+    float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
+    auto add = [&](int n, float wv, const Float8& ov) {
         if (n == 0) {
-            acc = make_float4(wv * ov.x, wv * ov.y, wv * ov.z, wv * ov.w);
+            a0 = make_float4(wv * ov.a.x, wv * ov.a.y, wv * ov.a.z, wv * ov.a.w);
+            a1 = make_float4(wv * ov.b.x, wv * ov.b.y, wv * ov.b.z, wv * ov.b.w);
         } else {
-            acc.x += wv * ov.x;
-            acc.y += wv * ov.y;
-            acc.z += wv * ov.z;
-            acc.w += wv * ov.w;
+            a0.x += wv * ov.a.x;
+            a0.y += wv * ov.a.y;
+            a0.z += wv * ov.a.z;
+            a0.w += wv * ov.a.w;
+            a1.x += wv * ov.b.x;
+            a1.y += wv * ov.b.y;
+            a1.z += wv * ov.b.z;
+            a1.w += wv * ov.b.w;
         }
     };
     if (k <= kCombineUnroll) {
@@ -553,37 +569,42 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             pos[n] = -1;
             wv[n] = 0.0f;
             if (n < k) {
-                const int64_t q = static_cast<int64_t>(t) * k + corder[static_cast<int64_t>(t) * k + n];
+                const int64_t q = base + corder[base + n];
                 pos[n] = pair_pos[q];
                 wv[n] = wts[q];
             }
         }
-        float4 ov[kCombineUnroll];
+        Float8 ov[kCombineUnroll];
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
             if (n < k && pos[n] >= 0 && pos[n] < P)  // never false for ids from k_topk; guards caller-supplied ids
-                ov[n] = load4(o + static_cast<int64_t>(pos[n]) * H + r);
+                ov[n] = load8(o + static_cast<int64_t>(pos[n]) * H + r);
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
             if (n < k && pos[n] >= 0 && pos[n] < P) add(n, wv[n], ov[n]);
     } else {
         for (int n = 0; n < k; n++) {
-            const int s = corder[static_cast<int64_t>(t) * k + n];
-            const int64_t q = static_cast<int64_t>(t) * k + s;
+            const int64_t q = base + corder[base + n];
             const int pos = pair_pos[q];
             if (pos < 0 || pos >= P) continue;
-            add(n, wts[q], load4(o + static_cast<int64_t>(pos) * H + r));
+            add(n, wts[q], load8(o + static_cast<int64_t>(pos) * H + r));
         }
     }
     if (o_sh) {
         const float gv = sg ? sg[t] : 1.0f;
-        const float4 sv = load4(o_sh + static_cast<int64_t>(t) * H + r);
-        acc.x += gv * sv.x;
-        acc.y += gv * sv.y;
-        acc.z += gv * sv.z;
-        acc.w += gv * sv.w;
+        const Float8 sv = load8(o_sh + static_cast<int64_t>(t) * H + r);
+        a0.x += gv * sv.a.x;
+        a0.y += gv * sv.a.y;
+        a0.z += gv * sv.a.z;
+        a0.w += gv * sv.a.w;
+        a1.x += gv * sv.b.x;
+        a1.y += gv * sv.b.y;
+        a1.z += gv * sv.b.z;
+        a1.w += gv * sv.b.w;
     }
-    *reinterpret_cast<float4*>(y + static_cast<int64_t>(t) * H + r) = acc;
+    float* out = y + static_cast<int64_t>(t) * H + r;
+    *reinterpret_cast<float4*>(out) = a0;
+    *reinterpret_cast<float4*>(out + 4) = a1;
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -902,8 +923,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         if (rc) return rc;
     }
     mark(5);
-    const int64_t threads = tokens * (L.hidden / 4);
-    const unsigned cgrid = static_cast<unsigned>((threads + 255) / 256);
+    const unsigned cgrid = static_cast<unsigned>(tokens * ((L.hidden + kCombineSpan - 1) / kCombineSpan));
     if (mfma)
         k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
                                                   w.wts, reinterpret_cast<const uint16_t*>(w.o),
