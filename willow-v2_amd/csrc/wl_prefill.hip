@@ -530,8 +530,8 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
 // row_ptr(item, r, lr), for nitems row sets one after another) and the tile's up to TILE tokens as NT token tiles of
 // 16 (NT = TILE / 16, 8, 4 or 1, the fewest that cover `count`; only those are staged). Per K chunk of 256 values
 // (one block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes kRT
-// A-fragments and runs kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in src ([*, ld] bf16);
-// rows past count load token 0's (their results are never stored).
+// A-fragments and runs kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in
+// src ([*, ld] bf16); rows past count load token 0's (their results are never stored).
 template <int TYPE, int TILE, typename RowPtr, typename SrcRow, typename Epilogue>
 __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][TILE / 16],
                                           int nblocks, int nitems, int count, const uint16_t* __restrict__ src,
