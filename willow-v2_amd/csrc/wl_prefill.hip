@@ -93,7 +93,8 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
         for (int q = 0; q < kXq; q++) xn[q] = *reinterpret_cast<const float4*>(xrow[q] + sgi * kRouterSeg);
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + sgi * kRouterSeg) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + sgi * kRouterSeg)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     const int lt = lane & 15, lj = lane >> 4;
     const int tm0 = 16 * TM * (wv & 1), rn0 = 32 * (wv >> 1);
@@ -151,7 +152,8 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
 #pragma unroll
             for (int n = 0; n < 2; n++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) tot[m][n][i] = sgi == 0 ? acc[m][n][i] : __fadd_rn(tot[m][n][i], acc[m][n][i]);
+                for (int i = 0; i < 4; i++)
+                    tot[m][n][i] = sgi == 0 ? acc[m][n][i] : __fadd_rn(tot[m][n][i], acc[m][n][i]);
     }
     // lane holds D[4 lj + i][lt]: token tm0 + 16 m + 4 lj + i, row rn0 + 16 n + lt
 #pragma unroll
@@ -525,13 +527,93 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     wait_stage();
 }
 
+// The K loop for tiles of at most 64 tokens (NT <= 4), whose steps have little arithmetic, so that each step's
+// weight round trip would otherwise be exposed: the row states run kRing - 1 steps ahead in a ring of registers
+// (the step loop is unrolled by kRing so every ring index is a constant), and the activation chunks are staged a
+// phase at a time: every chunk of the row set at once when they fit in the LDS buffers (then once for all items),
+// else kSlots chunks per phase, each phase staged, waited for and then computed. Only the row-state loads are in
+// flight while a phase computes, and they are ordinary loads, so the compiler's own waits before each ring entry's
+// first use are exact. Same results as gemm_loop: the same fragments and MFMAs in the same order.
+constexpr int kRing = 3;
+template <int TYPE, int TILE, int NT, int NTA, typename RowPtr, typename Epilogue>
+__device__ __forceinline__ void gemm_loop_small(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][NTA],
+                                                int nblocks, int nitems, const uint8_t* src, const uint32_t* rowtab,
+                                                RowPtr row_ptr, Epilogue epi, int lr, int q) {
+    constexpr int kChunk = NT * kGemmWaves * 1024;               // one staged chunk: NT token tiles
+    constexpr int kSlots = 2 * tile_bytes<TILE>() / kChunk;      // chunks the two buffers hold
+    static_assert(NT <= 4 && kSlots >= 2, "");
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
+    const uint32_t lds0 = lds_address(bufs[0]);
+    const uint8_t* base = bufs[0];
+    const BAddr ba = b_addr<TYPE>(lr, q);
+    const bool resident = nblocks <= kSlots;
+    const int nsteps = nitems * nblocks;
+    RowState<TYPE> ring[kRing][kRT];
+    auto fetch = [&](RowState<TYPE> (&rs)[kRT], int st) {
+        const int item = st / nblocks, kc = st - item * nblocks;
+#pragma unroll
+        for (int r = 0; r < kRT; r++)
+            rs[r].fetch(row_ptr(item, r, lr) + static_cast<int64_t>(kc) * BlockInfo<TYPE>::bytes, q);
+    };
+#pragma unroll
+    for (int u = 0; u + 1 < kRing; u++)
+        if (u < nsteps) fetch(ring[u], u);
+    bf16x8 a0[kRT], a1[kRT], b[NT];
+    for (int st0 = 0; st0 < nsteps; st0 += kRing) {
+#pragma unroll
+        for (int u = 0; u < kRing; u++) {
+            const int st = st0 + u;
+            if (st >= nsteps) break;
+            const int item = st / nblocks, kc = st - item * nblocks;
+            const int slot = resident ? kc : kc % kSlots;
+            if (resident ? st == 0 : slot == 0) {
+                // a new phase: every wavefront is done with the previous phase's chunks before they are replaced
+                __syncthreads();
+                const int n = resident ? nblocks : min(kSlots, nblocks - kc);
+                for (int c = 0; c < n; c++)
+                    stage_async<TILE, NT>(lds0 + c * kChunk, src + static_cast<int64_t>(kc + c) * kTileRowBytes,
+                                          rowtab, col, wv, half);
+                wait_stage();
+                __syncthreads();
+            }
+            if (st + kRing - 1 < nsteps) fetch(ring[(u + kRing - 1) % kRing], st + kRing - 1);
+            const uint8_t* buf = base + slot * kChunk;
+            RowState<TYPE> (&rs)[kRT] = ring[u];
+            read_b<TYPE, NT, 0>(buf, ba, b);
+#pragma unroll
+            for (int r = 0; r < kRT; r++) {
+                rs[r].prepare(q);
+                a0[r] = rs[r].template frag<0>(q);
+            }
+            gemm_step<TYPE, NT, 0, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+            gemm_step<TYPE, NT, 1, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+            gemm_step<TYPE, NT, 2, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+            gemm_step<TYPE, NT, 3, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+            gemm_step<TYPE, NT, 4, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+            gemm_step<TYPE, NT, 5, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+            gemm_step<TYPE, NT, 6, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+            gemm_step<TYPE, NT, 7, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+            if (kc == nblocks - 1) {
+                epi(item, acc);
+#pragma unroll
+                for (int r = 0; r < kRT; r++)
+#pragma unroll
+                    for (int n = 0; n < NTA; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // The GEMM core: a workgroup of kGemmWaves wavefronts, each owning kRT row tiles of 16 (rows given by
 // row_ptr(item, r, lr), for nitems row sets one after another) and the tile's up to TILE tokens as NT token tiles of
 // 16 (NT = TILE / 16, 8, 4 or 1, the fewest that cover `count`; only those are staged). Per K chunk of 256 values
-// (one block per row) the activations sit in LDS, double-buffered, and each of the 8 32-value steps decodes kRT
-// A-fragments and runs kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in
-// src ([*, ld] bf16); rows past count load token 0's (their results are never stored).
+// (one block per row) the activations sit in LDS (double-buffered in gemm_loop; staged a phase at a time in
+// gemm_loop_small, which takes NT = 4 and 1), and each of the 8 32-value steps decodes kRT A-fragments and runs
+// kRT x NT MFMAs; epi(item, acc) stores each row set's results. src_row(t) is token t's row in src ([*, ld] bf16);
+// rows past count load token 0's (their results are never stored).
 template <int TYPE, int TILE, typename RowPtr, typename SrcRow, typename Epilogue>
 __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()], floatx4 (&acc)[kRT][TILE / 16],
                                           int nblocks, int nitems, int count, const uint16_t* __restrict__ src,
@@ -552,9 +634,9 @@ __device__ __forceinline__ void gemm_tile(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     else if (count > 64)
         gemm_loop<TYPE, TILE, 8, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
     else if (count > 16)
-        gemm_loop<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
+        gemm_loop_small<TYPE, TILE, 4, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
     else
-        gemm_loop<TYPE, TILE, 1, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
+        gemm_loop_small<TYPE, TILE, 1, NTA>(bufs, acc, nblocks, nitems, s8, rowtab, row_ptr, epi, lr, q);
 }
 
 // Workgroups are dealt to the 8 XCDs round-robin by linear id, each XCD with its own L2. slab_tile maps the linear
