@@ -255,7 +255,6 @@ __device__ void write_active(const int32_t* counts, int E, int32_t* __restrict__
     if (tid == 0) active[0] = *n_active;
 }
 
-// One chunk (T <= kSortChunk): everything in one workgroup.
 // With tiles non-null (the MFMA path), the sort's single-workgroup stage also writes the GEMMs' tile lists.
 struct TileOut {
     int4* tiles;
@@ -269,34 +268,6 @@ __device__ __forceinline__ void write_tiles(const TileOut& to, const int32_t* of
     __syncthreads();  // offsets[] written by this workgroup are visible to all of it
     tile_list(offsets, E, T, to.with_shared, kTileTokens, to.tiles, to.n_tiles, scan);
     tile_list(offsets, E, T, to.with_shared, kDownTileTokens, to.tiles_down, to.n_tiles + 1, scan);
-}
-
-__global__ __launch_bounds__(256) void k_sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
-                                                    int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                                    int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos,
-                                                    TileOut to) {
-    extern __shared__ uint32_t smem[];
-    uint32_t* bits = smem;
-    int32_t* counts = reinterpret_cast<int32_t*>(bits + E * kSortWords);
-    int32_t* offs = counts + E;
-    int32_t* flags = offs + E;
-    int32_t* scratch = flags + E;  // 2 * 256 + 1
-    const int tid = threadIdx.x, nt = blockDim.x;
-    chunk_bitmap(ids, 0, T, k, E, bits, counts);
-    for (int e = tid; e < E; e += nt) offs[e] = counts[e];
-    __syncthreads();
-    block_exclusive_scan(offs, E, scratch, nullptr);
-    for (int e = tid; e < E; e += nt) offsets[e] = offs[e];
-    if (tid == 0) offsets[E] = T * k;
-    write_active(counts, E, active, flags, scratch);
-    for (int q = tid; q < T * k; q += nt) {
-        const int e = ids[q];
-        if (e < 0 || e >= E) continue;
-        const int pos = offs[e] + chunk_rank(bits, e, q / k);
-        sorted[pos] = q;
-        pair_pos[q] = pos;
-    }
-    if (to.tiles) write_tiles(to, offsets, E, T);
 }
 
 // Many chunks: per-chunk ranks and counts, then one scan, then the scatter.
@@ -362,6 +333,99 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
     const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
     sorted[pos] = static_cast<int32_t>(p);
     pair_pos[p] = pos;
+}
+
+// One chunk (T <= kSortChunk), a workgroup of 1024 threads: one thread per expert builds the stable counting sort
+// (the same outputs as the multi-chunk path) and the GEMM tile lists from the LDS bitmaps, with workgroup scans
+// made of wavefront scans (three barriers each).
+constexpr int kSortSmallThreads = 1024;
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+// Exclusive prefix sum of one value per thread over the workgroup (thread order); *total = the sum. wsum holds one
+// int per wavefront. Ends with a barrier, so wsum can be used again at once.
+__device__ int block_scan_excl(int v, int* wsum, int* total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int inc = wave_incl_scan(v, lane);
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    if (wv == 0) {
+        int w = lane < nw ? wsum[lane] : 0;
+        w = wave_incl_scan(w, lane);
+        if (lane < nw) wsum[lane] = w;
+    }
+    __syncthreads();
+    const int r = (wv > 0 ? wsum[wv - 1] : 0) + inc - v;
+    *total = wsum[nw - 1];
+    __syncthreads();
+    return r;
+}
+
+// tile_list for thread e = expert e (count c, first position off), all threads taking part
+__device__ void tile_list_small(int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int cap, int e, int E,
+                                int c, int off, int T, int with_shared, int* wsum) {
+    int total;
+    int n = block_scan_excl(e < E ? (c + cap - 1) / cap : 0, wsum, &total);
+    if (e < E)
+        for (int p = 0; p < c; p += cap) tiles[n++] = make_int4(e, off + p, min(cap, c - p), 0);
+    if (with_shared)
+        for (int p = static_cast<int>(threadIdx.x) * cap; p < T; p += static_cast<int>(blockDim.x) * cap)
+            tiles[total + p / cap] = make_int4(E, p, min(cap, T - p), 0);
+    if (threadIdx.x == 0) n_tiles[0] = total + (with_shared ? (T + cap - 1) / cap : 0);
+}
+
+__global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t* __restrict__ ids, int T, int k,
+                                                                  int E, int32_t* __restrict__ offsets,
+                                                                  int32_t* __restrict__ active,
+                                                                  int32_t* __restrict__ sorted,
+                                                                  int32_t* __restrict__ pair_pos, TileOut to) {
+    __shared__ int32_t lds_ids[kSortChunk * WL_MAX_TOPK];
+    __shared__ uint32_t bits[kSortWords * 64 * kMaxEJ];  // expert e: words kSortWords e .. + kSortWords - 1
+    __shared__ int32_t lds_off[64 * kMaxEJ];
+    __shared__ int wsum[kSortSmallThreads / 64];
+    const int tid = threadIdx.x;
+    const int P = T * k;
+    for (int q = tid; q < P; q += blockDim.x) lds_ids[q] = ids[q];
+    for (int i = tid; i < kSortWords * E; i += blockDim.x) bits[i] = 0u;
+    __syncthreads();
+    for (int q = tid; q < P; q += blockDim.x) {
+        const int e = lds_ids[q], t = q / k;
+        if (e >= 0 && e < E) atomicOr(&bits[kSortWords * e + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    const int e = tid;
+    int c = 0;
+    if (e < E)
+#pragma unroll
+        for (int wd = 0; wd < kSortWords; wd++) c += __popc(bits[kSortWords * e + wd]);
+    int total;
+    const int off = block_scan_excl(c, wsum, &total);
+    if (e < E) {
+        offsets[e] = off;
+        lds_off[e] = off;
+    }
+    if (tid == 0) offsets[E] = P;
+    const int apos = block_scan_excl(c > 0 ? 1 : 0, wsum, &total);  // its barriers also publish lds_off
+    if (e < E && c > 0) active[1 + apos] = e;
+    if (tid == 0) active[0] = total;
+    for (int q = tid; q < P; q += blockDim.x) {
+        const int ex = lds_ids[q];
+        if (ex < 0 || ex >= E) continue;
+        const int pos = lds_off[ex] + chunk_rank(bits, ex, q / k);
+        sorted[pos] = q;
+        pair_pos[q] = pos;
+    }
+    if (to.tiles) {
+        tile_list_small(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list_small(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -719,9 +783,8 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
     const size_t scan_lds = sizeof(int32_t) * (3 * E + 2 * 256 + 1);
     if (nchunks == 1) {
-        const size_t lds = sizeof(uint32_t) * E * kSortWords + scan_lds;
-        k_sort_small<<<1, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted, w.pair_pos,
-                                         to);
+        k_sort_small<<<1, kSortSmallThreads, 0, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted,
+                                                     w.pair_pos, to);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
         k_sort_hist<<<nchunks, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
