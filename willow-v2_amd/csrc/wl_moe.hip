@@ -177,41 +177,8 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, 
 //   offsets[E+1]    first sorted position of each expert's pairs; offsets[E] = T*k
 //   active[0]       number of experts with at least one pair; active[1..] those experts, ascending
 //   sorted[P]       pair id (t*k + slot) at each sorted position;  pair_pos[P] the inverse
-__device__ void block_exclusive_scan(int32_t* a, int n, int32_t* scratch, int32_t* total_out) {
-    // n <= 4 * blockDim.x; scratch: 2 * blockDim.x ints of LDS
-    const int tid = threadIdx.x, nt = blockDim.x;
-    int local[4];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int idx = tid * 4 + i;
-        local[i] = idx < n ? a[idx] : 0;
-        sum += local[i];
-    }
-    int32_t* buf0 = scratch;
-    int32_t* buf1 = scratch + nt;
-    buf0[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < nt; off <<= 1) {
-        const int val = buf0[tid] + (tid >= off ? buf0[tid - off] : 0);
-        __syncthreads();
-        buf1[tid] = val;
-        __syncthreads();
-        int32_t* tmp = buf0;
-        buf0 = buf1;
-        buf1 = tmp;
-    }
-    int run = buf0[tid] - sum;  // exclusive prefix of this thread's group
-    if (tid == nt - 1 && total_out) *total_out = buf0[tid];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int idx = tid * 4 + i;
-        if (idx < n) a[idx] = run;
-        run += local[i];
-    }
-    __syncthreads();
-}
+// One chunk: k_sort_small. Many chunks: k_sort_hist (per-chunk bitmaps, counts and ranks) -> k_sort_scan (chunk
+// bases, offsets, active experts, tile lists) -> k_sort_scatter.
 
 // Bitmaps of one chunk; returns with counts[e] filled (LDS) and `bits` holding the chunk's bitmap.
 __device__ void chunk_bitmap(const int32_t* __restrict__ ids, int t_begin, int t_end, int k, int E, uint32_t* bits,
@@ -243,18 +210,6 @@ __device__ __forceinline__ int chunk_rank(const uint32_t* bits, int e, int t) {
     return r;
 }
 
-__device__ void write_active(const int32_t* counts, int E, int32_t* __restrict__ active, int32_t* flags,
-                             int32_t* scratch) {
-    const int tid = threadIdx.x, nt = blockDim.x;
-    for (int e = tid; e < E; e += nt) flags[e] = counts[e] > 0 ? 1 : 0;
-    __syncthreads();
-    int32_t* n_active = scratch + 2 * nt;
-    block_exclusive_scan(flags, E, scratch, n_active);
-    for (int e = tid; e < E; e += nt)
-        if (counts[e] > 0) active[1 + flags[e]] = e;
-    if (tid == 0) active[0] = *n_active;
-}
-
 // With tiles non-null (the MFMA path), the sort's single-workgroup stage also writes the GEMMs' tile lists.
 struct TileOut {
     int4* tiles;
@@ -263,14 +218,6 @@ struct TileOut {
     int with_shared;
 };
 
-__device__ __forceinline__ void write_tiles(const TileOut& to, const int32_t* offsets, int E, int T) {
-    __shared__ int scan[2][256];
-    __syncthreads();  // offsets[] written by this workgroup are visible to all of it
-    tile_list(offsets, E, T, to.with_shared, kTileTokens, to.tiles, to.n_tiles, scan);
-    tile_list(offsets, E, T, to.with_shared, kDownTileTokens, to.tiles_down, to.n_tiles + 1, scan);
-}
-
-// Many chunks: per-chunk ranks and counts, then one scan, then the scatter.
 __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int T, int k, int E,
                                                    int32_t* __restrict__ rank, int32_t* __restrict__ hist) {
     extern __shared__ uint32_t smem[];
@@ -288,37 +235,6 @@ __global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ i
         const int e = ids[p];
         rank[p] = (e >= 0 && e < E) ? chunk_rank(bits, e, q / k) : 0;
     }
-}
-
-__global__ __launch_bounds__(256) void k_sort_scan(int T, int k, int E, int nchunks, int32_t* __restrict__ hist,
-                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                                   TileOut to) {
-    extern __shared__ uint32_t smem[];
-    int32_t* counts = reinterpret_cast<int32_t*>(smem);
-    int32_t* offs = counts + E;
-    int32_t* flags = offs + E;
-    int32_t* scratch = flags + E;
-    const int tid = threadIdx.x, nt = blockDim.x;
-    for (int e = tid; e < E; e += nt) {
-        int run = 0;
-        for (int c = 0; c < nchunks; c++) {
-            const int64_t i = static_cast<int64_t>(c) * E + e;
-            const int b = hist[i];
-            hist[i] = run;
-            run += b;
-        }
-        counts[e] = run;
-        offs[e] = run;
-    }
-    __syncthreads();
-    block_exclusive_scan(offs, E, scratch, nullptr);
-    for (int e = tid; e < E; e += nt) {
-        offsets[e] = offs[e];
-        for (int c = 0; c < nchunks; c++) hist[static_cast<int64_t>(c) * E + e] += offs[e];
-    }
-    if (tid == 0) offsets[E] = T * k;
-    write_active(counts, E, active, flags, scratch);
-    if (to.tiles) write_tiles(to, offsets, E, T);
 }
 
 __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int T, int k, int E,
@@ -422,6 +338,62 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
         sorted[pos] = q;
         pair_pos[q] = pos;
     }
+    if (to.tiles) {
+        tile_list_small(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list_small(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+    }
+}
+
+// Many chunks: one thread per expert turns its per-chunk counts (hist[c][e]) into the chunk's first sorted
+// position, chunks read kScanBatch at a time with their loads issued together; offsets, active experts and tile
+// lists as in k_sort_small.
+constexpr int kScanBatch = 16;
+__global__ __launch_bounds__(kSortSmallThreads) void k_sort_scan(int T, int k, int E, int nchunks,
+                                                                 int32_t* __restrict__ hist,
+                                                                 int32_t* __restrict__ offsets,
+                                                                 int32_t* __restrict__ active, TileOut to) {
+    __shared__ int wsum[kSortSmallThreads / 64];
+    const int e = threadIdx.x;
+    const bool mine = e < E;
+    int pre[kScanBatch];  // with nchunks <= kScanBatch: the expert's per-chunk prefixes, kept for the second pass
+    int run = 0;
+    for (int c0 = 0; c0 < nchunks; c0 += kScanBatch) {
+        int v[kScanBatch];
+#pragma unroll
+        for (int u = 0; u < kScanBatch; u++)
+            v[u] = (mine && c0 + u < nchunks) ? hist[static_cast<int64_t>(c0 + u) * E + e] : 0;
+#pragma unroll
+        for (int u = 0; u < kScanBatch; u++) {
+            pre[u] = run;
+            if (mine && c0 + u < nchunks && nchunks > kScanBatch) hist[static_cast<int64_t>(c0 + u) * E + e] = run;
+            run += v[u];
+        }
+    }
+    const int c = mine ? run : 0;
+    int total;
+    const int off = block_scan_excl(c, wsum, &total);
+    if (mine) offsets[e] = off;
+    if (threadIdx.x == 0) offsets[E] = T * k;
+    if (mine) {
+        if (nchunks <= kScanBatch) {
+#pragma unroll
+            for (int u = 0; u < kScanBatch; u++)
+                if (u < nchunks) hist[static_cast<int64_t>(u) * E + e] = pre[u] + off;
+        } else {
+            for (int c0 = 0; c0 < nchunks; c0 += kScanBatch) {
+                int v[kScanBatch];
+#pragma unroll
+                for (int u = 0; u < kScanBatch; u++)
+                    v[u] = c0 + u < nchunks ? hist[static_cast<int64_t>(c0 + u) * E + e] : 0;
+#pragma unroll
+                for (int u = 0; u < kScanBatch; u++)
+                    if (c0 + u < nchunks) hist[static_cast<int64_t>(c0 + u) * E + e] = v[u] + off;
+            }
+        }
+    }
+    const int apos = block_scan_excl(c > 0 ? 1 : 0, wsum, &total);
+    if (mine && c > 0) active[1 + apos] = e;
+    if (threadIdx.x == 0) active[0] = total;
     if (to.tiles) {
         tile_list_small(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
         tile_list_small(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
@@ -781,15 +753,14 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
     const int E = L.n_experts, k = L.top_k;
     const TileOut to{tiles ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0};
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
-    const size_t scan_lds = sizeof(int32_t) * (3 * E + 2 * 256 + 1);
     if (nchunks == 1) {
         k_sort_small<<<1, kSortSmallThreads, 0, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted,
                                                      w.pair_pos, to);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
         k_sort_hist<<<nchunks, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
-        k_sort_scan<<<1, 256, scan_lds + sizeof(int32_t) * E, s>>>(static_cast<int>(T), k, E, nchunks, w.hist,
-                                                                   w.offsets, w.active, to);
+        k_sort_scan<<<1, kSortSmallThreads, 0, s>>>(static_cast<int>(T), k, E, nchunks, w.hist, w.offsets,
+                                                    w.active, to);
         const int64_t P = T * k;
         k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(ids, static_cast<int>(T), k, E, w.rank,
                                                                           w.hist, w.sorted, w.pair_pos);

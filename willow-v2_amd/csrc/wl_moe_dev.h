@@ -248,43 +248,4 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{a, b}, bf16x2));
 }
 
-// Tiles: each routed expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles of at
-// most `cap` tokens; tiles[i] = (expert, first position or token, count), n_tiles[0] = how many. One workgroup of
-// 256 threads, thread i owning experts 4i .. 4i + 3 (E <= 1024): tile counts, an exclusive scan of them across the
-// workgroup, then each thread writes its experts' tiles in expert order. Two lists, for the two GEMMs' tile sizes.
-__device__ inline void tile_list(const int32_t* __restrict__ offsets, int E, int T, int with_shared, int cap,
-                          int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int (&scan)[2][256]) {
-    const int tid = threadIdx.x;
-    int mine = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * tid + i;
-        mine += e < E ? (offsets[e + 1] - offsets[e] + cap - 1) / cap : 0;
-    }
-    int cur = 0;
-    __syncthreads();  // scan is free (a previous list's reads are done)
-    scan[0][tid] = mine;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-        const int v = scan[cur][tid] + (tid >= off ? scan[cur][tid - off] : 0);
-        scan[cur ^ 1][tid] = v;
-        cur ^= 1;
-        __syncthreads();
-    }
-    int n = scan[cur][tid] - mine;  // tiles before this thread's experts
-    const int total = scan[cur][255];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * tid + i;
-        if (e >= E) break;
-        const int b = offsets[e], c = offsets[e + 1] - b;
-        for (int p = 0; p < c; p += cap) tiles[n++] = make_int4(e, b + p, min(cap, c - p), 0);
-    }
-    int m = total;
-    if (with_shared)
-        for (int p = tid * cap; p < T; p += 256 * cap) tiles[total + p / cap] = make_int4(E, p, min(cap, T - p), 0);
-    if (with_shared) m += (T + cap - 1) / cap;
-    if (tid == 0) n_tiles[0] = m;
-}
-
 }  // namespace wl
