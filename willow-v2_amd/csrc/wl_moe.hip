@@ -218,7 +218,7 @@ struct TileOut {
     int with_shared;
 };
 
-__global__ __launch_bounds__(256) void k_sort_hist(const int32_t* __restrict__ ids, int T, int k, int E,
+__global__ __launch_bounds__(1024) void k_sort_hist(const int32_t* __restrict__ ids, int T, int k, int E,
                                                    int32_t* __restrict__ rank, int32_t* __restrict__ hist) {
     extern __shared__ uint32_t smem[];
     uint32_t* bits = smem;
@@ -758,7 +758,7 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
                                                      w.pair_pos, to);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
-        k_sort_hist<<<nchunks, 256, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
+        k_sort_hist<<<nchunks, 1024, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
         k_sort_scan<<<1, kSortSmallThreads, 0, s>>>(static_cast<int>(T), k, E, nchunks, w.hist, w.offsets,
                                                     w.active, to);
         const int64_t P = T * k;
