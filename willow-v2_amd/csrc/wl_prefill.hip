@@ -322,26 +322,31 @@ struct RowState<WL_TYPE_Q6_K> {
 };
 
 // ---------------------------------------------------------------------------------------------------------------
-// LDS tile of one K chunk: [128 tokens][256 values] bf16, 512 bytes per token, no padding; the 16-byte slot holding
-// values 8c .. 8c + 7 of token t is slot c ^ (t & 7) of the token's row, so the 8 tokens lr = 0..7 a B-fragment read
-// serves at once sit in 8 different bank groups.
+// LDS tile of one K chunk: [TILE tokens][256 values] bf16, 512 bytes per token, no padding; the 16-byte slot holding
+// values 8c .. 8c + 7 of token t is slot c ^ (t & m) of the token's row, m = swizzle<TYPE>() (7 or 15), so the
+// tokens a B-fragment read serves at once sit in different bank groups.
 //
 // B-fragment of token t = 16 n + lr and the 8 values of slot c (values 8 c .. 8 c + 7): byte address
-// 512 t + 16 (c ^ (lr & 7)) = 512 lr + 16 (c ^ (lr & 7)) + 8192 n.
+// 512 t + 16 (c ^ (lr & m)) = 512 lr + 16 (c ^ (lr & m)) + 8192 n.
 // Q4_K order, c = 8 q + 4 (KK & 1) + (KK >> 1); Q6_K order, c = 16 h + 4 t + 2 p + s (KK = 2 t + s, q = 2 h + p).
-// In both, XOR with lr & 7 changes only the low 3 bits: a per-lane base for each KK.
+// In both, the XOR changes only the low 4 bits: a per-lane base for each KK.
 template <int KK>
 constexpr int q4k_slot_low() { return 4 * (KK & 1) + (KK >> 1); }
 
+// The 16-byte slot c of token t sits at c ^ (t & swizzle): 8 tokens for Q4_K's B-fragment reads, 16 for Q6_K's
+// (their lane groups read different slot patterns; each mask is the one the LDS bank-conflict counter reads zero
+// for, measured on the MI355X).
+template <int TYPE>
+constexpr int swizzle() { return TYPE == WL_TYPE_Q4_K ? 7 : 15; }
 struct BAddr {
     uint32_t step[8];
 };
 template <int TYPE>
 __device__ __forceinline__ BAddr b_addr(int lr, int q) {
     BAddr ba{};
-    const int y = lr & 7;
+    const int y = lr & 7, y8 = (lr & swizzle<TYPE>()) >> 3;  // the swizzle's low 3 bits and its bit 3
     if constexpr (TYPE == WL_TYPE_Q4_K) {
-        const uint32_t base = 512u * lr + 128u * q;
+        const uint32_t base = 512u * lr + 128u * (q ^ y8);
         ba.step[0] = base + 16u * (q4k_slot_low<0>() ^ y);
         ba.step[1] = base + 16u * (q4k_slot_low<1>() ^ y);
         ba.step[2] = base + 16u * (q4k_slot_low<2>() ^ y);
@@ -356,7 +361,7 @@ __device__ __forceinline__ BAddr b_addr(int lr, int q) {
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int t = kk >> 1, sidx = kk & 1;
-            ba.step[kk] = base + 128u * (t >> 1) + 16u * ((4 * (t & 1) + 2 * p + sidx) ^ y);
+            ba.step[kk] = base + 128u * ((t >> 1) ^ y8) + 16u * ((4 * (t & 1) + 2 * p + sidx) ^ y);
         }
     }
     return ba;
@@ -410,8 +415,8 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, const BAddr& ba, c
 // Direct global -> LDS staging of a K chunk with gfx950's global_load_lds_dwordx4: one wavefront instruction writes
 // 64 consecutive 16-byte LDS slots (M0 + 16 lane), two token rows. With W = kGemmWaves, instruction `it` of
 // wavefront w fills rows 2 W it + 2 w + (lane >> 5); lane slot s = lane & 31 of row t takes the 16 bytes of values
-// 8 (s ^ (t & 7)) .. + 7, and t & 7 = (2 w + (lane >> 5)) & 7 does not depend on it (2 W is a multiple of 8), so
-// the lane's byte column `col` is fixed. The rows' byte offsets come from `rowtab`, laid out so that a lane's
+// 8 (s ^ (t & m)) .. + 7, and t & m = (2 w + (lane >> 5)) & m does not depend on it (2 W is a multiple of 16),
+// so the lane's byte column `col` is fixed. The rows' byte offsets come from `rowtab`, laid out so that a lane's
 // stage_iters (TILE / 16) are contiguous: rowtab[stage_iters (t % 2 W) + t / 2 W].
 //
 // The loads are issued from inline assembly so that the compiler, which cannot tell the two LDS buffers apart,
@@ -419,7 +424,7 @@ __device__ __forceinline__ void gemm_step(const uint8_t* buf, const BAddr& ba, c
 // (s_waitcnt vmcnt(0) and a barrier) before the buffer is read.
 template <int TILE>
 constexpr int stage_iters() { return tile_bytes<TILE>() / (kGemmWaves * 1024); }  // 9 for 144 tokens
-static_assert(kGemmWaves % 4 == 0 && kTileTokens % (2 * kGemmWaves) == 0 && kDownTileTokens % (2 * kGemmWaves) == 0,
+static_assert(kGemmWaves % 8 == 0 && kTileTokens % (2 * kGemmWaves) == 0 && kDownTileTokens % (2 * kGemmWaves) == 0,
               "");
 template <int TILE>
 __host__ __device__ constexpr int rowtab_index(int t) {
@@ -475,7 +480,7 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
                                           Epilogue epi, int lr, int q) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
-    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & swizzle<TYPE>()));
     const uint32_t lds0 = lds_address(bufs[0]), lds1 = lds_address(bufs[1]);
     const BAddr ba = b_addr<TYPE>(lr, q);
     RowState<TYPE> rs[kRT], nx[kRT];
@@ -544,7 +549,7 @@ __device__ __forceinline__ void gemm_loop_small(uint8_t (&bufs)[2][tile_bytes<TI
     static_assert(NT <= 4 && kSlots >= 2, "");
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
-    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & 7));
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & swizzle<TYPE>()));
     const uint32_t lds0 = lds_address(bufs[0]);
     const uint8_t* base = bufs[0];
     const BAddr ba = b_addr<TYPE>(lr, q);
