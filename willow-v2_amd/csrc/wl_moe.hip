@@ -284,8 +284,10 @@ __device__ int block_scan_excl(int v, int* wsum, int* total) {
     return r;
 }
 
-// tile_list for thread e = expert e (count c, first position off), all threads taking part
-__device__ void tile_list_small(int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int cap, int e, int E,
+// GEMM tiles: each routed expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles
+// of at most `cap` tokens; tiles[i] = (expert, first position or token, count, 0), n_tiles[0] = how many. Thread e
+// holds expert e's count c and first position off; every thread of the workgroup takes part (E <= blockDim.x).
+__device__ void tile_list(int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int cap, int e, int E,
                                 int c, int off, int T, int with_shared, int* wsum) {
     int total;
     int n = block_scan_excl(e < E ? (c + cap - 1) / cap : 0, wsum, &total);
@@ -339,8 +341,8 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
         pair_pos[q] = pos;
     }
     if (to.tiles) {
-        tile_list_small(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
-        tile_list_small(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
     }
 }
 
@@ -395,8 +397,8 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_scan(int T, int k, i
     if (mine && c > 0) active[1 + apos] = e;
     if (threadIdx.x == 0) active[0] = total;
     if (to.tiles) {
-        tile_list_small(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
-        tile_list_small(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
     }
 }
 
