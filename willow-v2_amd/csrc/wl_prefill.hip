@@ -54,8 +54,9 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
 // replay. A workgroup computes 32 TM tokens x 64 rows (rows: experts, then the shared gate as row E); wavefront w
 // the TM x 2 tiles of 16 x 16 at tokens 16 TM (w & 1) + 16 m and rows 32 (w >> 1) + 16 n. Per segment the operands
 // are staged in LDS as [j][token or row][s] with 20-float rows: lane (l % 16, j = l / 16) reads its 16 values of the
-// segment as four 16-byte loads, and the 8 lanes of one LDS cycle fall in 8 different bank groups. Segment s + 1 is
-// loaded into registers while segment s is computed.
+// segment as four 16-byte loads, and the 8 lanes of one LDS cycle fall in 8 different bank groups. The staging is
+// double-buffered: while segment s is computed, segment s + 1 is written to the other buffer and segment s + 2 is
+// loaded into registers, one barrier per segment.
 constexpr int kRmRow = 20;
 constexpr int kRouterMfmaTM = 1;  // token tiles of 16 per wavefront
 
@@ -67,8 +68,8 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
                                                      uint16_t* __restrict__ xb) {
     constexpr int kTok = 32 * TM;              // tokens per workgroup
     constexpr int kXq = kTok * 16 / 256;       // float4 loads per thread per segment (tokens)
-    __shared__ __attribute__((aligned(16))) float xs[4 * kTok * kRmRow];
-    __shared__ __attribute__((aligned(16))) float ws[4 * 64 * kRmRow];
+    __shared__ __attribute__((aligned(16))) float xs[2][4 * kTok * kRmRow];
+    __shared__ __attribute__((aligned(16))) float ws[2][4 * 64 * kRmRow];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.x * kTok, r0 = blockIdx.y * 64;
     const int rows = E + (shared_gate ? 1 : 0);
@@ -100,39 +101,46 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
     const int tm0 = 16 * TM * (wv & 1), rn0 = 32 * (wv >> 1);
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     floatx4 tot[TM][2], acc[TM][2];
-    load_seg(0);
-    for (int sgi = 0; sgi < nseg; sgi++) {
-        __syncthreads();
+    // staging of segment sgi (from registers) into LDS buffer sgi & 1, with x also stored as bf16 once per token
+    auto stage = [&](int sgi) {
+        float* xsb = xs[sgi & 1];
+        float* wsb = ws[sgi & 1];
 #pragma unroll
         for (int q = 0; q < kXq; q++) {
             const int rr = (tid + 256 * q) >> 4;
             if (xb && blockIdx.y == 0 && t0 + rr < T)  // x as bf16 for the MFMA GEMMs, written once per token
                 *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + sgi * kRouterSeg + 4 * s4) =
                     make_uint2(pack2(xn[q].x, xn[q].y), pack2(xn[q].z, xn[q].w));
-            xs[(0 * kTok + rr) * kRmRow + s4] = xn[q].x;
-            xs[(1 * kTok + rr) * kRmRow + s4] = xn[q].y;
-            xs[(2 * kTok + rr) * kRmRow + s4] = xn[q].z;
-            xs[(3 * kTok + rr) * kRmRow + s4] = xn[q].w;
+            xsb[(0 * kTok + rr) * kRmRow + s4] = xn[q].x;
+            xsb[(1 * kTok + rr) * kRmRow + s4] = xn[q].y;
+            xsb[(2 * kTok + rr) * kRmRow + s4] = xn[q].z;
+            xsb[(3 * kTok + rr) * kRmRow + s4] = xn[q].w;
         }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int rr = (tid + 256 * q) >> 4;
-            ws[(0 * 64 + rr) * kRmRow + s4] = wn[q].x;
-            ws[(1 * 64 + rr) * kRmRow + s4] = wn[q].y;
-            ws[(2 * 64 + rr) * kRmRow + s4] = wn[q].z;
-            ws[(3 * 64 + rr) * kRmRow + s4] = wn[q].w;
+            wsb[(0 * 64 + rr) * kRmRow + s4] = wn[q].x;
+            wsb[(1 * 64 + rr) * kRmRow + s4] = wn[q].y;
+            wsb[(2 * 64 + rr) * kRmRow + s4] = wn[q].z;
+            wsb[(3 * 64 + rr) * kRmRow + s4] = wn[q].w;
         }
-        __syncthreads();
-        if (sgi + 1 < nseg) load_seg(sgi + 1);
+    };
+    load_seg(0);
+    stage(0);
+    if (nseg > 1) load_seg(1);
+    __syncthreads();
+    for (int sgi = 0; sgi < nseg; sgi++) {
+        const float* xsb = xs[sgi & 1];
+        const float* wsb = ws[sgi & 1];
 #pragma unroll
         for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
             float4 av[TM], bv[2];
 #pragma unroll
             for (int m = 0; m < TM; m++)
-                av[m] = *reinterpret_cast<const float4*>(&xs[(lj * kTok + tm0 + 16 * m + lt) * kRmRow + 4 * q]);
+                av[m] = *reinterpret_cast<const float4*>(&xsb[(lj * kTok + tm0 + 16 * m + lt) * kRmRow + 4 * q]);
 #pragma unroll
             for (int n = 0; n < 2; n++)
-                bv[n] = *reinterpret_cast<const float4*>(&ws[(lj * 64 + rn0 + 16 * n + lt) * kRmRow + 4 * q]);
+                bv[n] = *reinterpret_cast<const float4*>(&wsb[(lj * 64 + rn0 + 16 * n + lt) * kRmRow + 4 * q]);
 #pragma unroll
             for (int u = 0; u < 4; u++) {
 #pragma unroll
@@ -147,6 +155,12 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
                 }
             }
         }
+        // the next segment goes into the other buffer, whose last reads (segment sgi - 1) ended before the barrier
+        // that closed the previous iteration; its loads were issued a segment ago
+        if (sgi + 1 < nseg) {
+            stage(sgi + 1);
+            if (sgi + 2 < nseg) load_seg(sgi + 2);
+        }
 #pragma unroll
         for (int m = 0; m < TM; m++)
 #pragma unroll
@@ -154,6 +168,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     tot[m][n][i] = sgi == 0 ? acc[m][n][i] : __fadd_rn(tot[m][n][i], acc[m][n][i]);
+        __syncthreads();  // segment sgi + 1 is staged for everyone; buffer sgi & 1 is free again
     }
     // lane holds D[4 lj + i][lt]: token tm0 + 16 m + 4 lj + i, row rn0 + 16 n + lt
 #pragma unroll
