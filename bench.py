@@ -274,6 +274,7 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-load", action="store_true")
+    ap.add_argument("--skip-linear", action="store_true")
     ap.add_argument("--load-layers", type=int, default=8,
                     help="full-shape layers in the synthetic GGUF file of the loader measurement")
     ap.add_argument("--no-graph", action="store_true",
@@ -358,6 +359,8 @@ def main():
         del d64
     if not args.skip_load:
         result["gguf_load"] = run_gguf_load(torch, args.load_layers)
+    if not args.skip_linear:
+        result["linear_q4k"] = run_linear(torch, hip)
     if not args.skip_cpu:
         log("timing the CPU oracle")
         result["cpu_baseline"] = cpu_baseline()
@@ -386,6 +389,35 @@ def run_prefill(torch, hip, layers, T, steps):
             "tflops": round(flops / ms / 1e9, 2), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
             "path": layers[0].plan(T) + ": tiled fp32 router, bf16 MFMA grouped expert GEMMs (in-register "
                     "Q4_K/Q6_K dequant), fp32 combine"}
+
+
+def run_linear(torch, hip, rows=2048, k=2048, T=4096, reps=20):
+    """A quantized non-expert weight in a 4096-token prefill: GGMLWeight's F.linear above 8 tokens, as wl_linear
+    (bf16 MFMA, weights dequantized in registers) and as the reference's form (dequantize_gpu to bf16, then a bf16
+    matmul; gguf/metal.py:407), timed with events over `reps` calls each."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    raw = gen_q4k(torch, rows * (k // 256), gen).view(-1)
+    x = torch.randn(T, k, device="cuda", generator=gen).to(torch.bfloat16)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1000.0 / reps
+
+    us_mfma = timed(lambda: hip.linear_mfma(raw, "Q4_K", (rows, k), x))
+    us_ref = timed(lambda: torch.nn.functional.linear(x, hip.dequantize_gpu(raw, "Q4_K", (rows, k))))
+    flops = 2.0 * T * rows * k
+    log(f"linear Q4_K {rows}x{k}, {T} tokens: wl_linear {us_mfma:.1f} us ({flops / us_mfma / 1e6:.0f} TFLOP/s), "
+        f"dequantize + bf16 matmul {us_ref:.1f} us")
+    return {"rows": rows, "k": k, "tokens": T, "us_wl_linear": round(us_mfma, 2),
+            "us_dequantize_matmul": round(us_ref, 2), "tflops_wl_linear": round(flops / us_mfma / 1e6, 1)}
 
 
 def run_gguf_load(torch, n_layers):

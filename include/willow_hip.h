@@ -66,6 +66,14 @@ int wl_dequant(int type, const void* w, int64_t rows, int64_t k, int64_t row_str
 int wl_gemv(int type, const void* w, int64_t rows, int64_t k, int64_t row_stride, const float* x, int64_t tokens,
             float* y, void* stream);
 
+/* y[t, r] = sum_k W[r, k] * x[t, k] for t < tokens on the bf16 matrix core: x bf16 [tokens x k] (row stride k),
+ * W's exact values rounded to bf16 in registers (never written out), fp32 accumulation, y bf16 [tokens x rows].
+ * rows and k multiples of 256; W dense rows (row stride = wl_row_bytes(type, k)), 16-byte aligned for Q4_K.
+ * Replaces the prefill branch of GGMLWeight.linear, gguf/metal.py:401-408 (dequantize_gpu to bf16, then a bf16
+ * F.linear), without the dequantized copy. */
+int wl_linear(int type, const void* w, int64_t rows, int64_t k, const uint16_t* x, int64_t tokens, uint16_t* y,
+              void* stream);
+
 /* For each i < n: out[positions_host[i], :] = W_i x, with W_i the [rows x k] matrix at byte offset
  * offsets_host[i] from `base`; x fp32 [k], out fp32 [*, rows]. offsets/positions are HOST arrays (n <=
  * WL_MAX_BATCH_EXPERTS) passed by value to the kernel. Replaces gguf/metal.py:336-343 (gemv_batch). */

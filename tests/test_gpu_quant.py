@@ -1,5 +1,6 @@
-"""GPU parity of the quantized kernels (wl_dequant, wl_gemv, wl_gemv_batch, wl_gemv_combine) against the CPU oracle.
-Dequantized weights must be bit-exact; products within the normwise bound 2e-3 (fp32 accumulation)."""
+"""GPU parity of the quantized kernels (wl_dequant, wl_gemv, wl_linear, wl_gemv_batch, wl_gemv_combine) against the
+CPU oracle. Dequantized weights must be bit-exact; products within the normwise bound 2e-3 (fp32 accumulation), or
+4e-3 for wl_linear, whose output is rounded to bf16 (2^-9 relative) as the reference's bf16 F.linear is."""
 import os
 
 import numpy as np
@@ -104,6 +105,30 @@ def test_ggml_weight_linear(hip):
         assert moe_ref.rel_err(y.cpu().numpy(), expect) < (TOL if tokens <= 8 else 2e-2)
     base, offset = weight.location()
     assert offset == 0 and base.numel() == w.size
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("rows,k", [(256, 256), (512, 2048), (2048, 512)])
+@pytest.mark.parametrize("tokens", [9, 20, 64, 65, 130, 300])
+def test_linear_mfma(hip, name, rows, k, tokens):
+    """wl_linear against bf16(x) . bf16(dequantized W)^T in fp64: token counts on each K-loop form (one, four and
+    eight token tiles of 16, and several 128-token tiles, the last one partial)."""
+    rng = np.random.default_rng(rows + k + tokens)
+    w = synth.matrix(rng, name, rows, k)
+    x = rng.standard_normal((tokens, k)).astype(np.float32)
+    y = hip.linear_mfma(dev(w).reshape(-1), name, (rows, k), torch.from_numpy(x).cuda())
+    assert y.dtype == torch.bfloat16 and y.shape == (tokens, rows)
+    wb = q.round_bf16(q.dequantize_matrix(w, name, rows, k)).astype(np.float64)
+    ref = q.round_bf16(x).astype(np.float64) @ wb.T
+    err = moe_ref.rel_err(y.float().cpu().numpy(), ref)
+    assert err < 4e-3, err
+
+
+def test_linear_mfma_rejects(hip):
+    w = torch.zeros(255 * 144, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(16, 256, device="cuda")
+    with pytest.raises(ValueError):  # rows not a multiple of 256
+        hip.linear_mfma(w, "Q4_K", (255, 256), x)
 
 
 def test_errors_raise(hip):

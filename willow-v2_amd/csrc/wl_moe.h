@@ -78,6 +78,7 @@ struct PrefillArgs {
     int H, inter, sh_inter, E, k;
     int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
     int down_slabs;          // 256-row slabs per down workgroup
+    int dense_tokens;        // > 0: k_gemm_down runs one matrix (down) over this many tokens, tiles implied
 };
 
 struct Workspace {
@@ -118,5 +119,7 @@ int max_tiles(const WlMoeLayer& L, int64_t T, int cap);
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s);
 int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s);
+int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x, int64_t T, uint16_t* y,
+                  hipStream_t s);
 
 }  // namespace wl

@@ -883,7 +883,7 @@ const char* wl_error_string(int code) {
     return "unknown error";
 }
 
-int wl_abi_version(void) { return (1 << 16) | 0; }
+int wl_abi_version(void) { return (1 << 16) | 1; }  // 1.1: wl_linear
 
 int wl_moe_check(const WlMoeLayer* layer) { return check_layer(layer); }
 

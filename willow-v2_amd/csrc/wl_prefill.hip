@@ -727,8 +727,15 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kDownTileTokens>()];
     int group, ti;
     slab_tile(a.H / 256 / a.down_slabs, group, ti);
-    if (ti >= a.n_tiles_down[0]) return;
-    const int4 tile = a.tiles_down[ti];
+    int4 tile;
+    if (a.dense_tokens > 0) {  // wl_linear: token tile ti of one matrix
+        const int p = ti * kDownTileTokens;
+        if (p >= a.dense_tokens) return;
+        tile = make_int4(0, p, min(kDownTileTokens, a.dense_tokens - p), 0);
+    } else {
+        if (ti >= a.n_tiles_down[0]) return;
+        tile = a.tiles_down[ti];
+    }
     const bool sh = tile.x == a.E;
     const int inter = sh ? a.sh_inter : a.inter;
     const int row0 = group * a.down_slabs * 256 + 16 * kRT * (threadIdx.x >> 6);
@@ -854,6 +861,29 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     return launch_status();
 }
 
+// y[t, :] = W x[t, :] for a single quantized matrix on the down GEMM: bf16 operands (x as given, W's exact values
+// rounded to bf16 in registers), fp32 accumulation, bf16 output. rows and k are multiples of 256.
+int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x, int64_t T, uint16_t* y,
+                  hipStream_t s) {
+    PrefillArgs a{};
+    a.down = w;
+    a.down_stride = 0;
+    a.h16 = const_cast<uint16_t*>(x);
+    a.o16 = y;
+    a.H = rows;
+    a.inter = k;
+    a.E = 1;  // the one matrix is expert 0, never the shared slot
+    a.down_slabs = 1;
+    a.dense_tokens = static_cast<int>(T);
+    const int tiles = static_cast<int>((T + kDownTileTokens - 1) / kDownTileTokens);
+    const dim3 grid(static_cast<unsigned>(rows / 256 * ((tiles + kXcds - 1) / kXcds * kXcds)));
+    if (type == WL_TYPE_Q4_K)
+        k_gemm_down<WL_TYPE_Q4_K><<<grid, kGemmThreads, 0, s>>>(a);
+    else
+        k_gemm_down<WL_TYPE_Q6_K><<<grid, kGemmThreads, 0, s>>>(a);
+    return launch_status();
+}
+
 bool prefill_eligible(const WlMoeLayer& L, int64_t T) {
     if (L.flags & WL_MOE_NO_MFMA) return false;
     // the reference's own split (gguf/metal.py:20,401-408): up to MAX_TOKENS tokens its exact-weight GEMV, above
@@ -870,3 +900,22 @@ bool prefill_eligible(const WlMoeLayer& L, int64_t T) {
 }
 
 }  // namespace wl
+
+extern "C" {
+
+int wl_linear(int type, const void* w, int64_t rows, int64_t k, const uint16_t* x, int64_t tokens, uint16_t* y,
+              void* stream) {
+    using namespace wl;
+    int rc = check_matrix(type, w, rows, k, wl_row_bytes(type, k));
+    if (rc) return rc;
+    if (!x || !y) return WL_EINVAL_NULL;
+    if (tokens <= 0 || rows % 256 != 0) return WL_EINVAL_SHAPE;
+    // the LDS staging addresses activation rows by 32-bit byte offsets
+    if (tokens * k * 2 >= (int64_t{1} << 31) || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16) return WL_EINVAL_ALIGN;
+    if (type == WL_TYPE_Q4_K && reinterpret_cast<uintptr_t>(w) % 16) return WL_EINVAL_ALIGN;
+    return launch_linear(type, static_cast<const uint8_t*>(w), static_cast<int>(rows), static_cast<int>(k), x,
+                         tokens, y, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

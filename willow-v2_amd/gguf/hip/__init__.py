@@ -65,6 +65,7 @@ def library() -> ctypes.CDLL:
     lib.wl_row_bytes.argtypes, lib.wl_row_bytes.restype = [c_int, i64], i64
     lib.wl_dequant.argtypes = [c_int, vp, i64, i64, i64, c_int, vp, vp]
     lib.wl_gemv.argtypes = [c_int, vp, i64, i64, i64, vp, i64, vp, vp]
+    lib.wl_linear.argtypes = [c_int, vp, i64, i64, vp, i64, vp, vp]
     lib.wl_gemv_batch.argtypes = [c_int, vp, i64, i64, i64p, i64p, c_int, vp, vp, vp]
     lib.wl_gemv_combine.argtypes = [c_int, vp, i64, i64, i64p, i64p, c_int, vp, vp, vp, vp]
     layer_p = ctypes.POINTER(WlMoeLayer)
@@ -78,7 +79,7 @@ def library() -> ctypes.CDLL:
     lib.wl_moe_plan.argtypes, lib.wl_moe_plan.restype = [layer_p, i64], c_int
     lib.wl_moe_workspace_init.argtypes, lib.wl_moe_workspace_init.restype = [vp, ctypes.c_size_t, vp], c_int
     lib.wl_moe_stage_name.argtypes, lib.wl_moe_stage_name.restype = [c_int], ctypes.c_char_p
-    for name in ("wl_dequant", "wl_gemv", "wl_gemv_batch", "wl_gemv_combine", "wl_moe_check", "wl_moe_route",
+    for name in ("wl_dequant", "wl_gemv", "wl_linear", "wl_gemv_batch", "wl_gemv_combine", "wl_moe_check", "wl_moe_route",
                  "wl_moe_layer", "wl_moe_layer_profile"):
         getattr(lib, name).restype = c_int
     _lib = lib
@@ -134,6 +135,19 @@ def gemv(raw: torch.Tensor, type_name: str, shape: tuple, x: torch.Tensor) -> to
     y = torch.empty(xf.shape[0], rows, dtype=torch.float32, device=raw.device)
     check(library().wl_gemv(_type_id(type_name), raw.data_ptr(), rows, k, row_bytes(type_name, k), xf.data_ptr(),
                             xf.shape[0], y.data_ptr(), _stream(raw.device)))
+    return y
+
+
+def linear_mfma(raw: torch.Tensor, type_name: str, shape: tuple, x: torch.Tensor) -> torch.Tensor:
+    """x [T, k] -> bf16 [T, rows] on the bf16 matrix core with the weights dequantized in registers: the numbers
+    of gguf/metal.py:407 (bf16 F.linear of the weight dequantized to bf16) without writing the bf16 weight out.
+    rows and k must be multiples of 256."""
+    rows, k = shape
+    _on_gpu(raw, "raw")
+    xb = x.reshape(-1, k).to(device=raw.device, dtype=torch.bfloat16).contiguous()
+    y = torch.empty(xb.shape[0], rows, dtype=torch.bfloat16, device=raw.device)
+    check(library().wl_linear(_type_id(type_name), raw.data_ptr(), rows, k, xb.data_ptr(), xb.shape[0], y.data_ptr(),
+                              _stream(raw.device)))
     return y
 
 
@@ -230,7 +244,9 @@ class GGMLWeight:
         flat = x.reshape(-1, x.shape[-1]).to(self.device)
         if flat.shape[0] <= MAX_TOKENS:
             y = gemv(self.raw, self.type_name, self.shape, flat).to(x.dtype)
-        else:
+        elif self.shape[0] % 256 == 0 and self.shape[1] % 256 == 0:
+            y = linear_mfma(self.raw, self.type_name, self.shape, flat).to(x.dtype)
+        else:  # the reference's own form (gguf/metal.py:407)
             y = F.linear(flat.to(torch.bfloat16), dequantize_gpu(self.raw, self.type_name, self.shape)).to(x.dtype)
         return y.view(*x.shape[:-1], y.shape[-1]).to(x.device)
 
