@@ -206,6 +206,25 @@ def test_prefill_mfma_c2(hip, c2, layer_c2):
     check_prefill(hip, c2, layer_c2, synth.tokens(600, 600), "c2 T=600")
 
 
+def test_prefill_full_chunk_sampled(hip, c2, layer_c2):
+    """The headline prefill chunk itself, 4096 tokens through the full-shape layer (tiled router, 16-chunk
+    grouping, full 144-token tiles): every token's expert ids and weights against the oracle, and the outputs of 24
+    sampled tokens, since a token's output depends on that token alone."""
+    from oracle import cref
+    T = 4096
+    x = synth.tokens(4096, T)
+    y, ids, wts = run_layer(hip, c2, x)
+    logits = cref.router_logits(x, layer_c2["router"], layer_c2.get("router_bias"))
+    wts_ref, ids_ref = moe_ref.route(logits, layer_c2["top_k"], layer_c2["norm_topk_prob"])
+    np.testing.assert_array_equal(ids, ids_ref)
+    np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
+    pick = np.sort(np.random.default_rng(5).choice(T, 24, replace=False))
+    y_ref = moe_ref.layer(x[pick], layer_c2, bf16_operands=True, bf16_outputs=True)
+    err = moe_ref.rel_err(y[pick], y_ref)
+    print(f"[prefill] full chunk T=4096, 24 sampled tokens: rel err {err:.2e}", flush=True)
+    assert err < TOL
+
+
 @pytest.mark.parametrize("variant", ["base", "q4k_down", "no_shared", "inter_256", "partial_tiles"])
 def test_prefill_mfma_variants(hip, variant):
     kw = dict(hidden=1024, inter=512, shared_inter=512, experts=16, top_k=4)
