@@ -131,7 +131,8 @@ def stage_bytes(stage, T, U, shared=True):
 
 
 def layer_bytes(T, U):
-    """The touched bytes of a layer for T tokens (BASELINE's accounting: experts + router + gate + x/y)."""
+    """The touched bytes of a layer for T tokens: the touched experts (U routed + the shared one), the fp32 router
+    and shared gate, x and y."""
     return (U + 1) * EXPERT_BYTES + ROUTER_BYTES + HIDDEN * 4 + T * HIDDEN * 4 * 2
 
 
@@ -284,7 +285,7 @@ def main():
                          "scaling FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build's MoE layer runs on a single MI355X (expert-parallel "
+        print("bench.py measures one GPU only: the MoE layer here runs on a single MI355X (expert-parallel "
               "sharding across GPUs is designed, not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch

@@ -6,8 +6,8 @@ gguf/metal.py:133-168), the router (engines/base.py:91-97, 448), SwiGLU experts 
 weighted combine with the sigmoid-gated shared expert (engines/base.py:445-490, 580-589).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only as the
-checker (or, for bench.py, as the timed CPU baseline). The product path (the gguf.hip package and
-libwillow_hip.so) never imports, links or calls anything here.
+reference that results are compared against (or, for bench.py, as the timed CPU baseline). The product path (the
+gguf.hip package and libwillow_hip.so) never imports, links or calls anything here.
 
 How each part is pinned (the reference ships no tests, fixtures or golden vectors for this path):
   quants_ref   two independent formulations (vectorized, from gguf/quants.py; per 32-value chunk, from
@@ -17,5 +17,5 @@ How each part is pinned (the reference ships no tests, fixtures or golden vector
   moe_ref      router logits replay the kernels' documented FMA order in C (bit-exact) and are checked against a
                float64 dot product within the fp32 error bound; route() against brute-force sorting; the layer
                against a float64 per-expert loop and against transformers' Qwen3_5MoeSparseMoeBlock on tiny
-               dequantized weights (third-party pin, run in the build container only).
+               dequantized weights (third-party pin; transformers is not needed where the GPU runs, so that test skips there).
 """
