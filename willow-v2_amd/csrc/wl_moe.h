@@ -25,13 +25,11 @@ constexpr int kFusedMaxG = 512;       // workgroups (one per CU)
 constexpr int kFusedMaxHidden = 2048; // model width
 constexpr int kFlagStride = 32;       // words between workgroups' epoch counters (one 128-byte line each)
 // fused decode kernel: its words at the start of the workspace: epoch counters, then the tagged 64-bit values
-// that cross workgroups (logits [E+1], shared-expert SwiGLU output [I], routed SwiGLU outputs [k, I], routed
-// down partial sums [k, H])
+// that cross workgroups (logits [E+1], shared-expert SwiGLU output [I], routed SwiGLU outputs [k, I])
 constexpr int kTagLogits = kFlagStride * kFusedMaxG;
 constexpr int kTagHsh = kTagLogits + 2 * (kFusedMaxE + 16);
 constexpr int kTagH = kTagHsh + 2 * kFusedMaxInter;
-constexpr int kTagP = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
-constexpr int kSyncWords = kTagP + 2 * kFusedMaxK * kFusedMaxHidden;
+constexpr int kSyncWords = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
 
 struct ExpertArgs {
     const uint8_t* gate_up;

@@ -11,19 +11,20 @@
 //   phase B   every wavefront issues the loads of its gate_up tasks (a gate row and its up row of one picked
 //             expert) at once, kept as raw words; while they are in flight the owners dot their shared down rows
 //             with h_shared; then the gate_up rows are decoded and dotted, and h (silu(g) * u) published;
-//   down      every wavefront requests its 8 rows of one picked expert's down matrix (workgroup chunks of 64 rows),
-//             which arrive while h crosses workgroups; a workgroup gathers the h of its chunk's expert only
-//             (I values), dots its 64 rows and publishes the partial sums P[slot][row];
-//   combine   each owner gathers the k partials of its 8 rows and writes y = sum_e w_e P_e + sg * shared_down h_sh,
-//             experts in ascending id.
-// fused_eligible requires a grid large enough for one pass: at most one down chunk and one owner group per
-// workgroup and kGateUpTasks gate_up tasks per wavefront (Qwen3.6's shapes on 256 CUs use every workgroup).
+//   down      workgroup b owns output rows 8b .. 8b + 7; its wavefront s < k requests those 8 rows of the s-th
+//             picked expert's down matrix, which arrive while h crosses workgroups, gathers that expert's h
+//             (I values, polled by the wavefront alone) and dots its rows into LDS;
+//   combine   in the same workgroup: y = sum_e w_e P_e + sg * shared_down h_sh for its 8 rows, experts in
+//             ascending id. Only the logits, h_shared and h cross workgroups.
+// fused_eligible requires a grid large enough for one pass: one owner group per workgroup and kGateUpTasks
+// gate_up tasks per wavefront (Qwen3.6's shapes on 256 CUs use every workgroup).
 // Every CU streams its share of the routed experts' bytes: gate_up rows as soon as the routing is known, down rows
-// as soon as its gate_up work is done.
+// as soon as its gate_up work is done (requested earlier, they would wait in the CU's load queues ahead of the
+// gate_up arithmetic).
 // The arithmetic (router_row, the top-k's picks and weights, the gate_up and down dot products, the combine
 // order) is the multi-kernel path's.
 //
-// No barriers: every value that crosses workgroups (logits, h_shared, h, P) is a 64-bit word (tag << 32 | bits)
+// No barriers: every value that crosses workgroups (logits, h_shared, h) is a 64-bit word (tag << 32 | bits)
 // written and read with relaxed device-scope atomics (single-copy atomic, bypassing the per-XCD L2s). The tag is
 // this call's epoch, so a consumer polls the data itself until every word it needs carries the current tag.
 // Each workgroup keeps its own epoch counter (one 128-byte line each, incremented as it exits), so all agree on
@@ -41,8 +42,7 @@ namespace wl {
 constexpr int kFusedThreads = 512;
 constexpr int kFusedWaves = kFusedThreads / 64;
 constexpr int kGateUpTasks = 2;  // gate_up tasks a wavefront has in flight at once (G = 256: all of them)
-constexpr int kChunkRows = 64;   // routed down rows per workgroup chunk (8 per wavefront)
-constexpr int kOwnRows = 8;      // output rows per owner group: shared down rows and the final sum
+constexpr int kOwnRows = 8;      // output rows per owner group: the shared and routed down rows and the final sum
 constexpr uint32_t kSpinLimit = 1u << 20;
 static_assert(kFusedThreads >= kFusedMaxE && kFusedMaxE % 32 == 0 && kFusedMaxE / 32 >= kFusedMaxK,
               "the top-k gives every logit a thread and needs at least k groups of 32");
@@ -61,7 +61,7 @@ struct FusedArgs {
     float* y;
     int32_t* ids_out;
     float* wts_out;
-    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I], P [k, H]
+    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I]
     int H, I, E, k, renorm, G;
 };
 
@@ -97,11 +97,37 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
     }
 }
 
+// The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. All Q loads of a polling
+// round are issued before any is checked.
+template <int Q, typename Src, typename Dst>
+__device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_t tag, Src src, Dst dst) {
+    static_assert(Q <= 32, "");
+    const int lane = threadIdx.x & 63;
+    uint32_t pending = Q == 32 ? 0xFFFFFFFFu : (1u << Q) - 1u;
+    for (uint32_t spins = 0;; spins++) {
+        uint64_t w[Q];
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            w[q] = (pending >> q) & 1u ? __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(lane + 64 * q)),
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0;
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (((pending >> q) & 1u) && static_cast<uint32_t>(w[q] >> 32) == tag) {
+                *dst(lane + 64 * q) = __builtin_bit_cast(float, static_cast<uint32_t>(w[q]));
+                pending &= ~(1u << q);
+            }
+        if (__all(pending == 0)) return true;
+        if (spins >= kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 template <int GU, int DN, int EJ, int NBD>
 __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     constexpr int WIDTH = 8 * NBD;  // lanes per down row (8 per block)
     constexpr int R = 64 / WIDTH;   // down rows per wavefront pass
-    __shared__ float lds_h[kFusedMaxInter];
+    __shared__ float lds_h[kFusedMaxK][kFusedMaxInter];  // the h of each picked expert (wavefront s: slot s)
     __shared__ float lds_hsh[kFusedMaxInter];
     __shared__ float lds_logits[kFusedMaxE + 1];
     __shared__ int lds_sel[kFusedMaxK];
@@ -332,11 +358,6 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         }
     }
-    const int chunks_per_expert = H / kChunkRows;
-    const bool has_chunk = b < k * chunks_per_expert;
-    const int cs = b / chunks_per_expert;  // the chunk's expert slot
-    auto chunk_row = [&](int pass) { return (b % chunks_per_expert) * kChunkRows + 8 * wv + R * pass + drow; };
-    RawLane<DN> draw[NBD];
 
     // the shared expert's down rows of this workgroup's owner group, while the loads above are in flight
     float sgv = 1.0f;
@@ -367,43 +388,42 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
     }
 
-    // down: the chunk's rows are requested only now (so far the gate_up rows had the bandwidth to themselves) and
-    // arrive while h crosses workgroups; then the h of the chunk's expert, 64 row dots, the partials published
-    if (has_chunk) {
-        const uint8_t* w = a.down + static_cast<int64_t>(expert_of(cs)) * a.down_stride;
+    // down: wavefront s < k takes the owner's rows of the s-th picked expert. They are requested only now (so far
+    // the gate_up rows had the bandwidth and the load queues to themselves) and arrive while h crosses workgroups;
+    // then the wavefront gathers that expert's h, dots its 8 rows and leaves the sums in LDS
+    if (owner && wv < k) {
+        auto own_row = [&](int pass) { return kOwnRows * b + R * pass + drow; };
+        RawLane<DN> draw[NBD];
+        const uint8_t* w = a.down + static_cast<int64_t>(expert_of(wv)) * a.down_stride;
 #pragma unroll
         for (int p = 0; p < NBD; p++)
-            draw[p].fetch(w + static_cast<int64_t>(chunk_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
-        ok = gather_tagged(
-                 a.sync, I, tag, [&](int i) { return kTagH + 2 * (cs * I + i); }, [&](int i) { return &lds_h[i]; }) &&
+            draw[p].fetch(w + static_cast<int64_t>(own_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
+        float* hs = lds_h[wv];
+        ok = gather_tagged_wave<4 * NBD>(
+                 a.sync, tag, [&](int i) { return kTagH + 2 * (wv * I + i); }, [&](int i) { return &hs[i]; }) &&
              ok;
+        lane_sync();
 #pragma unroll
         for (int p = 0; p < NBD; p++) {
-            Lane32 w;
-            draw[p].unpack(c, w);
+            Lane32 wr;
+            draw[p].unpack(c, wr);
             float4 hl[4], hh[4];
-            load_run(lds_h + lo, hl);
-            load_run(lds_h + hi, hh);
-            const float v = group_sum<WIDTH>(lane_dot(w, hl, hh));
-            if ((lane % WIDTH) == 0) put_tagged(a.sync, kTagP + 2 * (cs * H + chunk_row(p)), tag, v);
+            load_run(hs + lo, hl);
+            load_run(hs + hi, hh);
+            const float v = group_sum<WIDTH>(lane_dot(wr, hl, hh));
+            if ((lane % WIDTH) == 0) lds_p[wv * kOwnRows + R * p + drow] = v;
         }
     }
 
     // combine: the owner's rows y[j] = sum_s w_s P[s][j] (+ sg * shared), s in ascending expert id
-    if (owner) {
-        ok = gather_tagged(
-                 a.sync, k * kOwnRows, tag,
-                 [&](int i) { return kTagP + 2 * ((i / kOwnRows) * H + kOwnRows * b + i % kOwnRows); },
-                 [&](int i) { return &lds_p[i]; }) &&
-             ok;
-        if (threadIdx.x < kOwnRows) {
-            const int r = threadIdx.x;
-            float acc = 0.0f;
-            for (int s = 0; s < k; s++)
-                acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
-            if (shared) acc = acc + sgv * lds_sh[r];
-            a.y[kOwnRows * b + r] = ok ? acc : __builtin_nanf("");
-        }
+    const bool all_ok = __syncthreads_and(ok);
+    if (owner && threadIdx.x < kOwnRows) {
+        const int r = threadIdx.x;
+        float acc = 0.0f;
+        for (int s = 0; s < k; s++)
+            acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
+        if (shared) acc = acc + sgv * lds_sh[r];
+        a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
     }
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -464,12 +484,11 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T) {
     if (L.shared_gate_up && (L.shared_inter != L.inter || L.shared_gate_up_type != L.gate_up_type ||
                              L.shared_down_type != L.down_type))
         return false;
-    if (L.hidden % kChunkRows != 0 || L.hidden > kFusedMaxHidden) return false;
-    // one pass per workgroup: a down chunk and an owner group each at most, kGateUpTasks per wavefront at most
+    if (L.hidden % kOwnRows != 0 || L.hidden > kFusedMaxHidden) return false;
+    // one pass per workgroup: an owner group at most, kGateUpTasks per wavefront at most
     const int G = fused_grid();
-    const int64_t chunks = static_cast<int64_t>(L.top_k) * (L.hidden / kChunkRows);
     const int64_t tasks = static_cast<int64_t>(L.top_k) * L.inter;
-    return G >= 1 && chunks <= G && L.hidden / kOwnRows <= G && tasks <= static_cast<int64_t>(kGateUpTasks) * kFusedWaves * G;
+    return G >= 1 && L.hidden / kOwnRows <= G && tasks <= static_cast<int64_t>(kGateUpTasks) * kFusedWaves * G;
 }
 
 int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,
