@@ -52,6 +52,14 @@ __device__ __forceinline__ float half_to_float(uint32_t bits) {
 // byte n of w as a float (v_cvt_f32_ubyteN)
 __device__ __forceinline__ float ubyte(uint32_t w, int n) { return static_cast<float>((w >> (8 * n)) & 0xFFu); }
 
+// Hides w's bits from the optimizer. Run words masked to one field per byte (w & 0x0F0F0F0F) through it, or the
+// mask is folded into each byte's extraction (a v_bfe_u32 per value before v_cvt_f32_ubyte0) instead of staying
+// one instruction per 4 values, with v_cvt_f32_ubyteN reading the bytes in place.
+__device__ __forceinline__ uint32_t opaque(uint32_t w) {
+    __asm__("" : "+v"(w));
+    return w;
+}
+
 // 16 bytes from a 2-byte-aligned address, read as 5 aligned dwords and realigned with v_alignbyte. Every caller
 // stays inside its 210-byte Q6_K block: the extra bytes read lie at most 2 before and 4 after the 16 wanted ones,
 // and the ranges used (ql: block offsets 0..131, qh: 126..195) are inside the block.
@@ -112,8 +120,8 @@ __device__ __forceinline__ void decode_q4k(const uint8_t* __restrict__ blk, int 
     const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        o.lo[i] = q[i] & 0x0F0F0F0Fu;
-        o.hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+        o.lo[i] = opaque(q[i] & 0x0F0F0F0Fu);
+        o.hi[i] = opaque((q[i] >> 4) & 0x0F0F0F0Fu);
     }
 }
 
@@ -135,8 +143,8 @@ __device__ __forceinline__ void decode_q6k(const uint8_t* __restrict__ blk, int 
     const uint32_t sh = 2 * t0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        o.lo[i] = (l4[i] & 0x0F0F0F0Fu) | (((h2[i] >> sh) & 0x03030303u) << 4);
-        o.hi[i] = ((l4[i] >> 4) & 0x0F0F0F0Fu) | (((h2[i] >> (sh + 4)) & 0x03030303u) << 4);
+        o.lo[i] = opaque((l4[i] & 0x0F0F0F0Fu) | (((h2[i] >> sh) & 0x03030303u) << 4));
+        o.hi[i] = opaque(((l4[i] >> 4) & 0x0F0F0F0Fu) | (((h2[i] >> (sh + 4)) & 0x03030303u) << 4));
     }
 }
 
@@ -172,8 +180,8 @@ struct RawLane<WL_TYPE_Q4_K> {
         const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            o.lo[i] = q[i] & 0x0F0F0F0Fu;
-            o.hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+            o.lo[i] = opaque(q[i] & 0x0F0F0F0Fu);
+            o.hi[i] = opaque((q[i] >> 4) & 0x0F0F0F0Fu);
         }
     }
 };
@@ -208,8 +216,8 @@ struct RawLane<WL_TYPE_Q6_K> {
         for (int i = 0; i < 4; i++) {
             const uint32_t l4 = __builtin_amdgcn_alignbyte(l[i + 1], l[i], lsh);
             const uint32_t h2 = __builtin_amdgcn_alignbyte(h[i + 1], h[i], hsh);
-            o.lo[i] = (l4 & 0x0F0F0F0Fu) | (((h2 >> sh) & 0x03030303u) << 4);
-            o.hi[i] = ((l4 >> 4) & 0x0F0F0F0Fu) | (((h2 >> (sh + 4)) & 0x03030303u) << 4);
+            o.lo[i] = opaque((l4 & 0x0F0F0F0Fu) | (((h2 >> sh) & 0x03030303u) << 4));
+            o.hi[i] = opaque(((l4 >> 4) & 0x0F0F0F0Fu) | (((h2 >> (sh + 4)) & 0x03030303u) << 4));
         }
     }
 };

@@ -808,10 +808,15 @@ int max_tiles(const WlMoeLayer& L, int64_t T, int cap) {
 
 // 256-row slabs per down workgroup: several when there are enough tiles to fill the GPU with fewer workgroups, so
 // that each pays its pipeline start (and, with inter <= 512, its activation staging) once for several slabs.
+// Up to kDownFewTokens tokens (batched decode) always two: the grid is sized by the tile bound, most of its
+// workgroups find no tile, and with one workgroup per CU those are dispatched only as the working ones finish
+// (64 tokens, Zipf routing: 85.3 us per layer against 87.4 with one slab, 100.2 with four).
 constexpr int64_t kDownMinGroups = 1024;
+constexpr int64_t kDownFewTokens = 256;
 static int down_slabs(const WlMoeLayer& L, int64_t T) {
     const int nslab = L.hidden / 256;
     const int64_t tiles = max_tiles(L, T, kDownTileTokens) - L.n_experts;  // about the full tiles
+    if (T <= kDownFewTokens && nslab % 2 == 0) return 2;
     int p = 1;
     while (p < kDownSlabsMax && nslab % (2 * p) == 0 && tiles * nslab / (2 * p) >= kDownMinGroups) p *= 2;
     return p;
