@@ -403,14 +403,15 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                  a.sync, tag, [&](int i) { return kTagH + 2 * (wv * I + i); }, [&](int i) { return &hs[i]; }) &&
              ok;
         lane_sync();
+        float4 hl[4], hh[4];  // the lane's two runs of h: the same in every pass
+        load_run(hs + lo, hl);
+        load_run(hs + hi, hh);
+        const float shl = sum16(hl), shh = sum16(hh);
 #pragma unroll
         for (int p = 0; p < NBD; p++) {
             Lane32 wr;
             draw[p].unpack(c, wr);
-            float4 hl[4], hh[4];
-            load_run(hs + lo, hl);
-            load_run(hs + hi, hh);
-            const float v = group_sum<WIDTH>(lane_dot(wr, hl, hh));
+            const float v = group_sum<WIDTH>(lane_dot_s(wr, hl, hh, shl, shh));
             if ((lane % WIDTH) == 0) lds_p[wv * kOwnRows + R * p + drow] = v;
         }
     }
