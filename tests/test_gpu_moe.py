@@ -124,10 +124,11 @@ def c2_fp32(hip, layer_c2):
     return hip.MoELayer.from_host(layer_c2, mfma="never")
 
 
-@pytest.mark.parametrize("T", [2, 7, 8, 9, 64])
+@pytest.mark.parametrize("T", [2, 7, 8, 9, 64, 256, 257])
 def test_layer_c2_batches(hip, c2, layer_c2, T):
     """Up to 8 tokens the fp32 expert kernels, from 9 the bf16 MFMA GEMMs (checked against the bf16-operand
-    oracle)."""
+    oracle). 256 and 257 tokens sit either side of the down GEMM's switch from two 256-row slabs per workgroup to
+    the tile-count rule."""
     check_layer(hip, c2, layer_c2, synth.tokens(100 + T, T), f"c2 b={T}")
 
 
