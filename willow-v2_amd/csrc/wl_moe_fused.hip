@@ -97,12 +97,21 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
     }
 }
 
-// The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. All Q loads of a polling
-// round are issued before any is checked.
+// The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. It first waits on the last
+// value of each lane only (64 words instead of 64 Q per round), then gathers them all: an expert's last h values
+// come from the highest-numbered workgroups, which start last, so by the time those are in, nearly all of them
+// are, and the bulk polls no longer load the memory system while the producers finish (17.90 -> 17.60 us per
+// layer). All Q loads of a polling round are issued before any is checked.
 template <int Q, typename Src, typename Dst>
 __device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_t tag, Src src, Dst dst) {
     static_assert(Q <= 32, "");
     const int lane = threadIdx.x & 63;
+    for (uint32_t spins = 0; spins < kSpinLimit; spins++) {
+        const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(lane + 64 * (Q - 1))),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__all(static_cast<uint32_t>(w >> 32) == tag)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
     uint32_t pending = Q == 32 ? 0xFFFFFFFFu : (1u << Q) - 1u;
     for (uint32_t spins = 0;; spins++) {
         uint64_t w[Q];
