@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
                                                      const float* __restrict__ bias,
                                                      const float* __restrict__ shared_gate, int T, int H, int E,
                                                      float* __restrict__ logits, float* __restrict__ sg,
-                                                     uint16_t* __restrict__ xb) {
+                                                     uint16_t* __restrict__ xb, const float* __restrict__ gate_row) {
     constexpr int kTok = 32 * TM;              // tokens per workgroup
     constexpr int kXq = kTok * 16 / 256;       // float4 loads per thread per segment (tokens)
     __shared__ __attribute__((aligned(16))) float xs[2][4 * kTok * kRmRow];
@@ -188,6 +188,17 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
                 }
             }
         }
+    // gate_row: the shared gate when it has no row in the tiles. The workgroups of one token tile share its tokens,
+    // two per wavefront (one per half), in router_row's order, after their matrix-core work. This replaces a kernel
+    // of its own (10.8 us per 4096-token layer): 22.25 -> 21.95 ms per 40-layer chunk.
+    if (gate_row) {
+        for (int tt = static_cast<int>(blockIdx.y) * 8; tt < kTok; tt += static_cast<int>(gridDim.y) * 8) {
+            const int t = t0 + tt + 2 * wv + (lane >> 5);
+            const bool valid = t < T;
+            const float total = router_row(x + static_cast<int64_t>(valid ? t : 0) * H, gate_row, valid, H, lane);
+            if ((lane & 31) == 0 && valid) sg[t] = sigmoid(total);
+        }
+    }
 }
 
 
@@ -779,21 +790,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
 
 // ---------------------------------------------------------------------------------------------------------------
 
-// The shared gate's logit for many tokens when it would be the lone row of an extra router tile: a wavefront per
-// two tokens (one per half), router_row's order.
-__global__ __launch_bounds__(256) void k_router_sg(const float* __restrict__ x, const float* __restrict__ shared_gate,
-                                                   int T, int H, float* __restrict__ sg) {
-    const int lane = threadIdx.x & 63;
-    const int t = 2 * (blockIdx.x * 4 + (threadIdx.x >> 6)) + (lane >> 5);
-    const bool valid = t < T;
-    const float total = router_row(x + static_cast<int64_t>(valid ? t : 0) * H, shared_gate, valid, H, lane);
-    if ((lane & 31) == 0 && valid) sg[t] = sigmoid(total);
-}
-
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s) {
     const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
-    // with whole 64-row tiles of experts the shared gate gets its own small kernel instead of a 1-row tile
+    // with whole 64-row tiles of experts the shared gate is computed by the workgroups' VALU (gate_row) instead of
+    // as a 1-row tile
     const bool separate = shared_gate && L.n_experts % 64 == 0;
     const float* tiled_gate = separate ? nullptr : shared_gate;
     const int rows = L.n_experts + (tiled_gate ? 1 : 0);
@@ -801,10 +802,7 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
     k_router_mfma<kRouterMfmaTM><<<dim3(static_cast<unsigned>((T + 32 * kRouterMfmaTM - 1) / (32 * kRouterMfmaTM)),
                                         rtiles),
                                    256, 0, s>>>(x, L.router, L.router_bias, tiled_gate, static_cast<int>(T), L.hidden,
-                                                L.n_experts, logits, sg, xb);
-    if (separate)
-        k_router_sg<<<static_cast<unsigned>((T + 7) / 8), 256, 0, s>>>(x, shared_gate, static_cast<int>(T),
-                                                                       L.hidden, sg);
+                                                L.n_experts, logits, sg, xb, separate ? shared_gate : nullptr);
     return launch_status();
 }
 
