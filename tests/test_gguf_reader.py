@@ -1,6 +1,7 @@
-"""The GGUF header reader and the expert scan (gguf/reader.py, gguf/compiler.py:24-88 of the reference), on the
-CPU. The reader is pinned on a header assembled byte by byte here from the published GGUF layout (not by this
-package's writer); the writer, the split-file handling and the scan are then checked on files the writer makes."""
+"""The GGUF header reader and the expert index (gguf/reader.py, gguf/experts.py; the reference's counterparts are
+gguf/reader.py and the expert scan of gguf/compiler.py:24-88), on the CPU. The reader is pinned on a header
+assembled byte by byte here from the published GGUF layout (not by this package's writer); the writer, the
+split-file handling and the index are then checked on files the writer makes."""
 import os
 import struct
 
@@ -8,8 +9,8 @@ import numpy as np
 import pytest
 
 from gguf import synth
-from gguf.compiler import fuse_gate_up, num_decoder_layers, scan_experts
-from gguf.reader import (BLOCK_SIZES, GGML_TYPES, model_stem, read_gguf, read_gguf_file, split_paths,
+from gguf.experts import ExpertLayoutError, decoder_layer_count, index_experts
+from gguf.reader import (BLOCK_SIZES, GGML_TYPES, GGUFFormatError, read_gguf, read_gguf_file, shard_files,
                          tensor_nbytes)
 from gguf.writer import write_gguf
 
@@ -49,16 +50,31 @@ def test_reader_on_handmade_header(tmp_path):
     assert (a.shape, a.type, a.offset, a.nbytes) == ((3, 4), "F32", data_start, 48)
     # two rows of 512 Q4_K values: 2 x 2 blocks of 144 bytes
     assert (b.shape, b.type, b.offset, b.nbytes) == ((2, 512), "Q4_K", data_start + 64, 576)
-    assert a.path == b.path == str(p)
+    assert a.file == b.file == str(p)
 
 
-@pytest.mark.parametrize("bad", ["magic", "version", "type"])
+def test_reader_needs_more_than_the_first_read(tmp_path):
+    """A header longer than the reader's first piece (a large vocabulary array) is read in further pieces."""
+    big = s("tok.scores") + struct.pack("<I", 9) + struct.pack("<IQ", 6, 400_000) + bytes(4 * 400_000)
+    head = handmade_header()
+    n_kv = struct.unpack_from("<Q", head, 16)[0]
+    head = head[:16] + struct.pack("<Q", n_kv + 1) + head[24:]
+    kv_end = head.index(s("t.f32"))
+    head = head[:kv_end] + big + head[kv_end:]
+    p = tmp_path / "big.gguf"
+    p.write_bytes(head + bytes(4096))
+    md, ts = read_gguf_file(str(p))
+    assert len(md["tok.scores"]) == 400_000 and md["a.f64"] == 0.25
+    assert ts["t.q"].offset == (len(head) + 63) // 64 * 64 + 64
+
+
+@pytest.mark.parametrize("bad", ["magic", "version", "type", "truncated"])
 def test_reader_rejects(tmp_path, bad):
     head = {"magic": handmade_header(magic=b"GGUX"), "version": handmade_header(version=1),
-            "type": handmade_header(type_b=99)}[bad]
+            "type": handmade_header(type_b=99), "truncated": handmade_header()[:-9]}[bad]
     p = tmp_path / "bad.gguf"
-    p.write_bytes(head + bytes(128))
-    with pytest.raises(SystemExit):
+    p.write_bytes(head + (b"" if bad == "truncated" else bytes(128)))
+    with pytest.raises(GGUFFormatError):
         read_gguf_file(str(p))
 
 
@@ -101,15 +117,16 @@ def test_split_files(tmp_path):
     b = str(tmp_path / "M-Q4_K_M-00002-of-00002.gguf")
     synth.write_moe_gguf(a, [lw])
     write_gguf(b, {"split.count": 2}, [("blk.0.extra.weight", "F32", (4,), np.ones(4, np.float32))])
-    assert split_paths(b) == [a, b]
-    assert model_stem(b) == str(tmp_path / "M-Q4_K_M")
-    assert model_stem(str(tmp_path / "x.gguf")) == str(tmp_path / "x")
-    md, ts = read_gguf(b)
+    assert shard_files(b) == [a, b] and shard_files(a) == [a, b]
+    assert shard_files(str(tmp_path / "x.gguf")) == [str(tmp_path / "x.gguf")]
+    header = read_gguf(b)
+    md, ts = header
+    assert header.files == [a, b]
     assert md["general.architecture"] == "qwen35moe"          # the first file's metadata
-    assert ts["blk.0.extra.weight"].path == b and ts["blk.0.ffn_down_exps.weight"].path == a
+    assert ts["blk.0.extra.weight"].file == b and ts["blk.0.ffn_down_exps.weight"].file == a
     os.remove(b)
-    with pytest.raises(SystemExit):
-        split_paths(a)
+    with pytest.raises(FileNotFoundError):
+        shard_files(a)
 
 
 def small_layers(down_types=("Q6_K", "Q4_K"), experts=4):
@@ -117,36 +134,43 @@ def small_layers(down_types=("Q6_K", "Q4_K"), experts=4):
                             down_type=dt) for i, dt in enumerate(down_types)]
 
 
-def test_scan_experts_and_fuse(tmp_path):
+def test_index_experts(tmp_path):
     layers = small_layers()
     p = str(tmp_path / "m.gguf")
     synth.write_moe_gguf(p, layers + [layers[0]], extra_metadata={"qwen35moe.nextn_predict_layers": 1})
     md, ts = read_gguf(p)
-    assert num_decoder_layers(md) == 2  # the appended multi-token-prediction layer is skipped
-    n_layers, n_exp, max_payload, plan, info = scan_experts(md, ts)
+    assert decoder_layer_count(md) == 2  # the appended multi-token-prediction layer is skipped
+    index = index_experts(md, ts)
     gate_bytes = 256 * 144  # 256 rows of one Q4_K block
-    assert (n_layers, n_exp) == (2, 4)
-    assert info["0.down"] == {"shape": [256, 256], "dtype": "Q6_K"} and info["1.down"]["dtype"] == "Q4_K"
-    assert max_payload == 2 * gate_bytes + 256 * 210
+    assert [lay.layer for lay in index] == [0, 1]
+    assert [(lay.n_experts, lay.hidden, lay.inter) for lay in index] == [(4, 256, 256)] * 2
+    assert [(lay.gate_up_type, lay.down_type) for lay in index] == [("Q4_K", "Q6_K"), ("Q4_K", "Q4_K")]
+    assert index[0].gate_up_bytes == 2 * gate_bytes and index[0].down_bytes == 256 * 210
     raw = np.fromfile(p, dtype=np.uint8)
-    for (layer, e), parts in plan.items():
-        assert [q[0] for q in parts] == ["gate", "up", "down"]
-        t = ts[f"blk.{layer}.ffn_gate_exps.weight"]
-        assert parts[0][2] == t.offset + e * gate_bytes and parts[0][3] == gate_bytes
-        got = raw[parts[0][2]:parts[0][2] + gate_bytes]
-        assert got.tobytes() == layers[layer]["gate_up"][e, :256].tobytes()
-    fplan, finfo = fuse_gate_up(plan, info)
-    assert finfo["0.gate_up"] == {"shape": [512, 256], "dtype": "Q4_K"} and "0.gate" not in finfo
-    (part, srcs), (dpart, dsrc) = fplan[(1, 2)]
-    assert part == "gate_up" and dpart == "down" and len(srcs) == 2
-    fused = b"".join(raw[o:o + n].tobytes() for _, o, n in srcs)
-    assert fused == layers[1]["gate_up"][2].tobytes()
+    for lay in index:
+        for e in range(4):
+            ranges = lay.gate_up_ranges(e)
+            assert [size for _, _, size in ranges] == [gate_bytes, gate_bytes]
+            fused = b"".join(raw[o:o + n].tobytes() for _, o, n in ranges)
+            assert fused == layers[lay.layer]["gate_up"][e].tobytes()  # gate rows, then up rows
+            _, o, n = lay.down_range(e)
+            assert raw[o:o + n].tobytes() == layers[lay.layer]["down"][e].tobytes()
 
 
-def test_scan_rejects_dense_layers(tmp_path):
+@pytest.mark.parametrize("bad", ["dense_layer", "gate_up_mismatch", "down_shape"])
+def test_index_rejects(tmp_path, bad):
     layers = small_layers()
+    if bad == "gate_up_mismatch":  # up stored in another type than gate
+        layers[1] = synth.moe_layer(11, hidden=256, inter=256, shared_inter=256, experts=4, top_k=2)
     p = str(tmp_path / "m.gguf")
-    synth.write_moe_gguf(p, layers, extra_metadata={"qwen35moe.block_count": 3})
+    extra = {"qwen35moe.block_count": 3} if bad == "dense_layer" else None
+    synth.write_moe_gguf(p, layers, extra_metadata=extra)
     md, ts = read_gguf(p)
-    with pytest.raises(SystemExit):
-        scan_experts(md, ts)
+    if bad == "gate_up_mismatch":
+        t = ts["blk.1.ffn_up_exps.weight"]
+        ts["blk.1.ffn_up_exps.weight"] = type(t)(t.name, "Q6_K", t.shape, t.file, t.offset, t.nbytes)
+    if bad == "down_shape":
+        t = ts["blk.0.ffn_down_exps.weight"]
+        ts["blk.0.ffn_down_exps.weight"] = type(t)(t.name, t.type, (4, 512, 128), t.file, t.offset, t.nbytes)
+    with pytest.raises(ExpertLayoutError):
+        index_experts(md, ts)

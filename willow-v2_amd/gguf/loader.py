@@ -1,7 +1,7 @@
 """A Qwen3.6 GGUF model's MoE weights straight into HBM, still quantized.
 
-The reference reads the header (gguf/reader.py), locates every expert (scan_experts / fuse_gate_up,
-gguf/compiler.py:29-88), copies the experts into an SSD pack for streaming (compile_pack, gguf/compiler.py:90-197),
+The reference reads the header (gguf/reader.py), locates every expert (gguf/compiler.py:29-88), copies the
+experts into an SSD pack for streaming (compile_pack, gguf/compiler.py:90-197),
 and dequantizes the other weights to bf16 in RAM (load_weights, engines/qwen36/loader.py:195-234). Here the experts
 of every layer go from the file into one device tensor per layer and part (the HBMExpertStore layout: gate_up
 [E, gate rows then up rows], down [E, rows]) with no pack in between, and the MoE block's other weights (router,
@@ -18,9 +18,9 @@ import numpy as np
 import torch
 
 from . import hip
-from .compiler import fuse_gate_up, num_decoder_layers, scan_experts
+from .experts import decoder_layer_count, index_experts
 from .hbm_store import HBMExpertStore, LayerExperts
-from .reader import read_gguf
+from .reader import GGUFHeader, read_gguf
 
 PREFIX = "model.language_model."  # Qwen35MoEEngine's weight-name prefix
 # llama.cpp names of the MoE block's non-routed tensors -> Hugging Face names (engines/qwen36/loader.py:37-41)
@@ -35,8 +35,12 @@ FP32_NAMES = ("mlp.gate.weight", "mlp.shared_expert_gate.weight")  # kept fp32 f
 
 
 def _header(model):
-    """(metadata, tensors) from a path or from read_gguf's result."""
-    return read_gguf(model) if isinstance(model, (str, os.PathLike)) else model
+    """(metadata, tensors) from a path, a GGUFHeader or a (metadata, tensors) pair."""
+    if isinstance(model, (str, os.PathLike)):
+        model = read_gguf(os.fspath(model))
+    if isinstance(model, GGUFHeader):
+        return model.metadata, model.tensors
+    return model
 
 
 def moe_config(model) -> dict:
@@ -47,7 +51,7 @@ def moe_config(model) -> dict:
     def get(key, default=None):
         return metadata.get(f"{arch}.{key}", default)
 
-    return {"num_hidden_layers": num_decoder_layers(metadata), "hidden_size": get("embedding_length"),
+    return {"num_hidden_layers": decoder_layer_count(metadata), "hidden_size": get("embedding_length"),
             "num_experts": get("expert_count"), "num_experts_per_tok": get("expert_used_count"),
             "norm_topk_prob": get("expert_weights_norm", True),
             "moe_intermediate_size": get("expert_feed_forward_length"),
@@ -151,33 +155,19 @@ class _Stager:
 
 def load_experts(model, device="cuda", chunk_bytes: int = 32 << 20, threads: int = 8) -> HBMExpertStore:
     """Every layer's routed experts in HBM: an HBMExpertStore whose layer l holds gate_up [E, gate rows then up
-    rows] and down [E, rows] exactly as the file's blocks (gate and up fused per expert as fuse_gate_up plans it)."""
+    rows] and down [E, rows], byte for byte the file's blocks."""
     metadata, tensors = _header(model)
-    num_layers, num_experts, _, plan, part_info = scan_experts(metadata, tensors)
-    plan, part_info = fuse_gate_up(plan, part_info)
     stager = _Stager(device, chunk_bytes, threads=threads)
     layers = []
     try:
-        for layer in range(num_layers):
-            gu, dn = part_info.get(f"{layer}.gate_up"), part_info[f"{layer}.down"]
-            if gu is None:
-                raise ValueError(f"layer {layer}: gate and up differ in shape or type "
-                                 f"({part_info.get(f'{layer}.gate')} vs {part_info.get(f'{layer}.up')}); "
-                                 "the expert kernels need them fused")
-            parts = [dict(plan[(layer, e)]) for e in range(num_experts)]
-            gu_src = [p["gate_up"] for p in parts]
-            dn_src = [p["down"] for p in parts]
-            gu_bytes = sum(s[2] for s in gu_src[0])
-            dn_bytes = dn_src[0][0][2]
-            gate_up = torch.empty(num_experts, gu_bytes, dtype=torch.uint8, device=device)
-            down = torch.empty(num_experts, dn_bytes, dtype=torch.uint8, device=device)
-            stager.add(gate_up, gu_src)  # gate rows then up rows (or the one fused source)
-            stager.add(down, dn_src)
-            inter, hidden = gu["shape"][0] // 2, gu["shape"][1]
-            if dn["shape"] != [hidden, inter]:
-                raise ValueError(f"layer {layer}: down has shape {dn['shape']}, expected {[hidden, inter]}")
-            layers.append(LayerExperts(gate_up=gate_up, down=down, gate_up_type=gu["dtype"], down_type=dn["dtype"],
-                                       hidden=hidden, inter=inter))
+        for lay in index_experts(metadata, tensors):
+            E = lay.n_experts
+            gate_up = torch.empty(E, lay.gate_up_bytes, dtype=torch.uint8, device=device)
+            down = torch.empty(E, lay.down_bytes, dtype=torch.uint8, device=device)
+            stager.add(gate_up, [lay.gate_up_ranges(e) for e in range(E)])
+            stager.add(down, [[lay.down_range(e)] for e in range(E)])
+            layers.append(LayerExperts(gate_up=gate_up, down=down, gate_up_type=lay.gate_up_type,
+                                       down_type=lay.down_type, hidden=lay.hidden, inter=lay.inter))
         stager.run()
     finally:
         stager.close()
@@ -187,7 +177,7 @@ def load_experts(model, device="cuda", chunk_bytes: int = 32 << 20, threads: int
 
 
 def _read(t) -> np.ndarray:
-    return np.fromfile(t.path, dtype=np.uint8, count=t.nbytes, offset=t.offset)
+    return np.fromfile(t.file, dtype=np.uint8, count=t.nbytes, offset=t.offset)
 
 
 def _dense(t) -> np.ndarray:
@@ -210,7 +200,7 @@ def load_moe_weights(model, device="cuda", prefix: str = PREFIX) -> dict:
     shared expert's gate/up/down as GGMLWeight when their type runs on the kernels (Q4_K, Q6_K), else dense bf16."""
     metadata, tensors = _header(model)
     weights = {}
-    for layer in range(num_decoder_layers(metadata)):
+    for layer in range(decoder_layer_count(metadata)):
         for gguf_name, hf_name in MOE_LAYER_NAMES.items():
             t = tensors.get(f"blk.{layer}.{gguf_name}")
             if t is None:

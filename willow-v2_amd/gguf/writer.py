@@ -3,8 +3,8 @@ benchmark), since no real checkpoint is available offline.
 
     write_gguf(path, metadata, tensors, alignment=32)
 metadata: {key: value}; a value is a str, bool, int (u32 if it fits, else i64), float (f32), a list of one of
-those, or an explicit (value_type, value) pair with the GGUF type ids of gguf/reader.py (SCALAR_FORMATS, STRING,
-ARRAY: then value = (item_type, list)). tensors: [(name, ggml type name, shape in PyTorch order, data)], data a
+those, or an explicit (value_type, value) pair with the GGUF value type ids of gguf/reader.py (VALUE_DTYPES,
+VALUE_STRING, VALUE_ARRAY: then value = (item_type, list)). tensors: [(name, ggml type name, shape in PyTorch order, data)], data a
 bytes-like or numpy array holding exactly tensor_nbytes(shape, type) bytes. Each tensor's data starts at a multiple
 of `alignment` from the data section, which itself starts at a multiple of `alignment`; an alignment other than
 32 is recorded as general.alignment.
@@ -13,9 +13,9 @@ import struct
 
 import numpy as np
 
-from .reader import ARRAY, DEFAULT_ALIGNMENT, GGML_TYPES, GGUF_MAGIC, SCALAR_FORMATS, STRING, tensor_nbytes
+from .reader import ALIGNMENT_DEFAULT, MAGIC, TYPE_IDS, VALUE_ARRAY, VALUE_DTYPES, VALUE_STRING, tensor_nbytes
 
-_TYPE_IDS = {name: tid for tid, (name, _, _) in GGML_TYPES.items()}
+STRING, ARRAY = VALUE_STRING, VALUE_ARRAY
 U32, I64, F32, BOOL = 4, 11, 6, 7
 
 
@@ -50,17 +50,17 @@ def _value(kind: int, value) -> bytes:
     if kind == ARRAY:
         item, items = value
         body = struct.pack("<IQ", item, len(items))
-        if item in SCALAR_FORMATS:
-            return body + struct.pack(f"<{len(items)}{SCALAR_FORMATS[item]}", *items)
+        if item in VALUE_DTYPES:
+            return body + np.asarray(items, dtype=VALUE_DTYPES[item]).tobytes()
         return body + b"".join(_value(item, v) for v in items)
-    return struct.pack("<" + SCALAR_FORMATS[kind], value)
+    return np.asarray(value, dtype=VALUE_DTYPES[kind]).tobytes()
 
 
 def write_gguf(path: str, metadata: dict, tensors: list, alignment: int = 32, version: int = 3):
     alignment = int(metadata.get("general.alignment", alignment))
-    if alignment != DEFAULT_ALIGNMENT and "general.alignment" not in metadata:
+    if alignment != ALIGNMENT_DEFAULT and "general.alignment" not in metadata:
         metadata = {**metadata, "general.alignment": (U32, alignment)}  # readers assume 32 without it
-    head = [GGUF_MAGIC, struct.pack("<IQQ", version, len(tensors), len(metadata))]
+    head = [MAGIC, struct.pack("<IQQ", version, len(tensors), len(metadata))]
     for key, value in metadata.items():
         kind, v = _infer(value)
         head += [_string(key), struct.pack("<I", kind), _value(kind, v)]
@@ -73,7 +73,7 @@ def write_gguf(path: str, metadata: dict, tensors: list, alignment: int = 32, ve
         offset = -(-offset // alignment) * alignment
         ne = tuple(reversed(shape))
         head += [_string(name), struct.pack(f"<I{len(ne)}Q", len(ne), *ne),
-                 struct.pack("<IQ", _TYPE_IDS[type_name], offset)]
+                 struct.pack("<IQ", TYPE_IDS[type_name], offset)]
         placed.append((offset, buf))
         offset += nbytes
     header = b"".join(head)
