@@ -107,8 +107,8 @@ typedef struct WlMoeLayer {
 } WlMoeLayer;
 
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */
-#define WL_MOE_NO_MFMA 2         /* flags: never take the bf16 MFMA prefill path (fp32 GEMV path instead) */
-#define WL_MOE_FORCE_MFMA 4      /* flags: take the MFMA prefill path at any token count (testing) */
+#define WL_MOE_NO_MFMA 2         /* flags: every expert on the fp32 GEMV kernels at any token count */
+#define WL_MOE_FORCE_MFMA 4      /* flags: every expert on the bf16 MFMA GEMMs at any token count (testing) */
 
 /* Checks a layer description without touching device memory; 0 or a WL_E* code. */
 int wl_moe_check(const WlMoeLayer* layer);
@@ -122,10 +122,16 @@ size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
  * stream): concurrent ones race. */
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
-/* Which path wl_moe_layer takes for `tokens` tokens: 1 = one fused persistent kernel (batch-1 decode at
- * Qwen3.6-like shapes), 2 = bf16 MFMA grouped expert GEMMs (more than 8 tokens: the reference's own split between
- * its exact-weight GEMV and a bf16 matmul of dequantized weights, gguf/metal.py:20,401-408), 0 = the fp32
- * multi-kernel path (router, top-k, grouping, gate_up, down, combine); -1 on an invalid layer. */
+/* Which path wl_moe_layer takes for `tokens` tokens; -1 on an invalid layer.
+ *   1 = one fused persistent kernel (batch-1 decode at Qwen3.6-like shapes);
+ *   0 = the multi-kernel path with every expert on the fp32 GEMV kernels (exact weights; up to 8 tokens no expert
+ *       can be given more than 8);
+ *   2 = the multi-kernel path with each expert placed by its own token count, as the reference's each_expert
+ *       hands F.linear only that expert's tokens (engines/base.py:566-571) and GGMLWeight.linear switches at
+ *       MAX_TOKENS = 8 (gguf/metal.py:20,404-407): an expert given more than 8 tokens (and the shared expert, which
+ *       sees every token) on the bf16 MFMA grouped GEMMs (weights rounded to bf16, bf16 gate/up/SwiGLU/output as
+ *       bf16 tensors round them, fp32 accumulation), the others on the fp32 GEMV kernels;
+ *   3 = every expert on the MFMA GEMMs (WL_MOE_FORCE_MFMA). */
 int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens);
 
 /* Router: logits = x W_r^T (+ bias) in a fixed floating-point order: hidden is cut into segments of 64

@@ -47,33 +47,62 @@ def sigmoid(v: np.ndarray) -> np.ndarray:
         return 1 / (1 + np.exp(-v))
 
 
+# Up to this many tokens F.linear on a quantized weight runs the exact-weight GEMV; above it, a bf16 matmul of the
+# weight dequantized to bf16 (gguf/metal.py:20,404-407).
+MAX_TOKENS = 8
+CHAINS = ("fp32", "bf16", "split")
+
+
 def expert_ffn(x: np.ndarray, gate_up_w: np.ndarray, down_w: np.ndarray, inter: int, dtype=np.float32,
-               bf16_operands: bool = False, bf16_output: bool = False) -> np.ndarray:
+               chain: str = "fp32") -> np.ndarray:
     """down(silu(gate x) * (up x)) for x [n, hidden], with dequantized fused gate_up [2*inter, hidden] (gate rows
-    first) and down [hidden, inter] (engines/base.py:99-102, :567-571). bf16_operands rounds x, the weights and
-    the SwiGLU output to bf16 before each product, as a bf16 matmul of dequantized weights does
-    (gguf/metal.py:407); bf16_output rounds the result to bf16 too, as that F.linear returns it."""
-    if bf16_operands:
-        x, gate_up_w, down_w = round_bf16(x), round_bf16(gate_up_w), round_bf16(down_w)
-    gu = x.astype(dtype) @ gate_up_w.astype(dtype).T
-    h = silu(gu[:, :inter]) * gu[:, inter:]
-    if bf16_operands:
-        h = round_bf16(h.astype(np.float32)).astype(dtype)
-    out = h @ down_w.astype(dtype).T
-    if bf16_output:
-        out = round_bf16(out.astype(np.float32)).astype(dtype)
-    return out
+    first) and down [hidden, inter] (engines/base.py:99-102, :567-571).
+
+    chain "fp32": exact weights and fp32 activations throughout (the GEMV numerics at fp32 inputs).
+    chain "bf16": the reference's prefill chain on bf16 tensors. x and the dequantized weights are rounded to bf16
+    (gguf/metal.py:407; gguf/quants.py:223); each F.linear accumulates in fp32 and returns bf16 (the gate and up
+    halves of gate_up's output, and down's output); F.silu(gate) returns bf16, and so does silu(gate) * up
+    (engines/base.py:568-570)."""
+    h = swiglu_hidden(x, gate_up_w, inter, dtype, chain)
+    if chain == "fp32":
+        return h @ down_w.astype(dtype).T
+    return round_bf16(h.astype(dtype) @ round_bf16(down_w).astype(dtype).T).astype(dtype)
 
 
-def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False, return_routing: bool = False,
-          bf16_shared: bool = None, bf16_outputs: bool = False):
+def swiglu_hidden(x: np.ndarray, gate_up_w: np.ndarray, inter: int, dtype=np.float32,
+                  chain: str = "fp32") -> np.ndarray:
+    """silu(gate x) * (up x), the input of an expert's down projection, in expert_ffn's chain."""
+    if chain == "fp32":
+        gu = x.astype(dtype) @ gate_up_w.astype(dtype).T
+        return silu(gu[:, :inter]) * gu[:, inter:]
+    if chain != "bf16":
+        raise ValueError(f"chain must be 'fp32' or 'bf16', not {chain!r}")
+    gu = round_bf16(round_bf16(x).astype(dtype) @ round_bf16(gate_up_w).astype(dtype).T)
+    gate, up = gu[:, :inter], gu[:, inter:]
+    return round_bf16(round_bf16(silu(gate)) * up)
+
+
+def layer(x: np.ndarray, lw: dict, dtype=np.float32, chain: str = "fp32", return_routing: bool = False,
+          shared_chain: str = None, counts=None, layer_tokens: int = None):
     """The whole MoE layer for x fp32 [T, hidden]; lw is a layer dict as synth.moe_layer builds it. Returns
-    y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values). bf16_operands
-    rounds the routed experts' operands to bf16 (expert_ffn); bf16_shared does the same for the shared expert
-    (default: as bf16_operands). bf16_outputs also rounds each expert's output to bf16 (the shared expert's only
-    with bf16_shared); the weighted sum stays fp32."""
-    if bf16_shared is None:
-        bf16_shared = bf16_operands
+    y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values).
+
+    chain picks each expert's numerics (expert_ffn): "fp32" or "bf16" for every expert, or "split", the
+    reference's own rule: in each_expert an expert's F.linear receives only the tokens routed to it
+    (engines/base.py:566-571), so an expert given more than MAX_TOKENS tokens takes the bf16 chain and the others
+    the exact-weight fp32 one (gguf/metal.py:404-407); the shared expert sees all T tokens. shared_chain overrides
+    the shared expert's (e.g. "fp32" for dense fp32 shared weights run by torch). The weighted sum over experts is
+    fp32, in ascending expert order. For x a sample of a larger call's tokens, counts ([n_experts], each expert's
+    tokens in the whole call) and layer_tokens (the call's token count) let "split" place the experts as that
+    call does."""
+    if chain not in CHAINS:
+        raise ValueError(f"chain must be one of {CHAINS}, not {chain!r}")
+
+    def pick(n_tokens: int) -> str:
+        if chain != "split":
+            return chain
+        return "bf16" if n_tokens > MAX_TOKENS else "fp32"
+
     hidden, inter, experts = lw["hidden"], lw["inter"], lw["experts"]
     x = np.ascontiguousarray(x, dtype=np.float32)
     logits = cref.router_logits(x, lw["router"], lw.get("router_bias"))
@@ -83,14 +112,16 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False
         token_idx, slot = np.nonzero(ids == expert)
         gate_up_w = dequantize_matrix(lw["gate_up"][expert], lw["gate_up_type"], 2 * inter, hidden)
         down_w = dequantize_matrix(lw["down"][expert], lw["down_type"], hidden, inter)
-        h = expert_ffn(x[token_idx], gate_up_w, down_w, inter, dtype, bf16_operands, bf16_outputs)
+        n_tok = len(token_idx) if counts is None else int(counts[expert])
+        h = expert_ffn(x[token_idx], gate_up_w, down_w, inter, dtype, pick(n_tok))
         np.add.at(y, token_idx, h * weights[token_idx, slot, None].astype(dtype))
     shared_gate = None
     if lw.get("shared_gate_up") is not None:
         s_inter = lw["shared_inter"]
         gate_up_w = dequantize_matrix(lw["shared_gate_up"], lw["shared_gate_up_type"], 2 * s_inter, hidden)
         down_w = dequantize_matrix(lw["shared_down"], lw["shared_down_type"], hidden, s_inter)
-        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype, bf16_shared, bf16_outputs and bf16_shared)
+        h = expert_ffn(x, gate_up_w, down_w, s_inter, dtype,
+                       shared_chain or pick(x.shape[0] if layer_tokens is None else layer_tokens))
         if lw.get("shared_gate") is not None:
             z = cref.router_logits(x, lw["shared_gate"][None, :])[:, 0]
             shared_gate = sigmoid(z.astype(np.float32)).astype(np.float32)
@@ -99,6 +130,13 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, bf16_operands: bool = False
     if return_routing:
         return y, ids, weights, shared_gate
     return y
+
+
+def topk_margins(logits: np.ndarray, top_k: int) -> np.ndarray:
+    """Per token, the gap between its top_k-th and (top_k + 1)-th largest logit: how far the selection is from a
+    tie (a gap of 0 is a tie, broken toward the lower expert id)."""
+    part = -np.sort(-logits, axis=-1)
+    return (part[:, top_k - 1] - part[:, top_k]).astype(np.float32)
 
 
 def rel_err(y: np.ndarray, y_ref: np.ndarray) -> float:

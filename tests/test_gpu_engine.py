@@ -60,9 +60,8 @@ def test_engine_moe_matches_oracle(small_layer, quantized_shared, tokens):
     x = synth.tokens(62 + tokens, tokens)
     y = eng.moe(torch.from_numpy(x).cuda(), 0, residual=None)
     assert y.shape == (tokens, 2048) and y.dtype == torch.float32
-    # more than 8 tokens: bf16 operands in the kernel's experts (a dense shared expert stays fp32 in torch)
-    bf16 = tokens > 8
-    ref = moe_ref.layer(x, lw, bf16_operands=bf16, bf16_shared=bf16 and quantized_shared, bf16_outputs=bf16)
+    # each expert by its own token count; a dense shared expert runs in torch on its fp32 weights
+    ref = moe_ref.layer(x, lw, chain="split", shared_chain=None if quantized_shared else "fp32")
     assert moe_ref.rel_err(y.cpu().numpy(), ref) < 2e-3
     yb = eng.moe(torch.from_numpy(x).cuda().to(torch.bfloat16), 0)
     assert yb.dtype == torch.bfloat16

@@ -26,7 +26,7 @@ def run_layer(hip, layer, x):
 
 
 def check_layer(hip, layer, lw, x, label):
-    if layer.plan(x.shape[0]) == "mfma":  # more than 8 tokens: bf16 operands, as the reference's own split
+    if layer.plan(x.shape[0]) in ("split", "mfma"):  # experts on the bf16 MFMA GEMMs: the bf16 chain
         return check_prefill(hip, layer, lw, x, label)
     print(f"[moe] {label}: T={x.shape[0]}", flush=True)
     y, ids, wts = run_layer(hip, layer, x)
@@ -86,7 +86,7 @@ def test_fused_matches_multi_kernel(hip, c2, layer_c2):
     its outputs up to the compiler's multiply-add contraction in the combine (~1e-6)."""
     multi = hip.MoELayer.from_host(layer_c2, fused=False)
     assert c2.plan(1) == "fused" and multi.plan(1) == "gemv" and c2.plan(2) == "gemv" and c2.plan(8) == "gemv"
-    assert c2.plan(9) == "mfma" and c2.plan(600) == "mfma"
+    assert c2.plan(9) == "split" and c2.plan(600) == "split"
     for seed in range(5):
         x = synth.tokens(200 + seed, 1)
         y_f, ids_f, w_f = run_layer(hip, c2, x)
@@ -126,9 +126,11 @@ def c2_fp32(hip, layer_c2):
 
 @pytest.mark.parametrize("T", [2, 7, 8, 9, 64, 256, 257])
 def test_layer_c2_batches(hip, c2, layer_c2, T):
-    """Up to 8 tokens the fp32 expert kernels, from 9 the bf16 MFMA GEMMs (checked against the bf16-operand
-    oracle). 256 and 257 tokens sit either side of the down GEMM's switch from two 256-row slabs per workgroup to
-    the tile-count rule."""
+    """Up to 8 tokens every expert on the fp32 GEMV kernels; from 9 each expert by its own token count (the shared
+    expert and experts with more than 8 tokens on the bf16 MFMA GEMMs, checked against the oracle's split chain).
+    At 9 and 64 tokens nearly every routed expert stays on GEMV; at 256 and 257 (8 pairs per expert on average)
+    both classes are large. 256 and 257 also sit either side of the down GEMM's switch from two 256-row slabs per
+    workgroup to the tile-count rule."""
     check_layer(hip, c2, layer_c2, synth.tokens(100 + T, T), f"c2 b={T}")
 
 
@@ -149,21 +151,25 @@ def test_layer_zipf_b64(hip):
     lw = synth.moe_layer(3, zipf_alpha=1.1)
     layer = hip.MoELayer.from_host(lw)
     x = synth.tokens(33, 64)
-    assert layer.plan(64) == "mfma"
+    assert layer.plan(64) == "split"
     check_layer(hip, layer, lw, x, "zipf b=64")
     check_layer(hip, hip.MoELayer.from_host(lw, mfma="never"), lw, x, "zipf b=64 fp32")
     _, ids, _ = run_layer(hip, layer, x)
     counts = np.bincount(ids.reshape(-1), minlength=256)
     assert counts.max() >= 32  # a hot expert sees at least half the tokens
     assert (counts > 0).sum() < 256
+    # both classes present: experts above 8 tokens on the MFMA GEMMs, the rest on GEMV
+    assert (counts > 8).sum() >= 4 and ((counts > 0) & (counts <= 8)).sum() >= 4
 
 
-@pytest.mark.parametrize("variant", ["no_shared", "no_shared_gate", "q4k_down", "topk1", "few_experts",
-                                     "hidden_1024", "inter_256_no_norm"])
+@pytest.mark.parametrize("variant", ["no_shared", "no_shared_gate", "q4k_down", "q6k_gate_up", "topk1",
+                                     "few_experts", "hidden_1024", "inter_256_no_norm"])
 def test_layer_variants(hip, variant):
     kw = dict(hidden=1024, inter=512, shared_inter=512, experts=32, top_k=4)
     if variant == "q4k_down":
         kw["down_type"] = "Q4_K"
+    if variant == "q6k_gate_up":  # Q6_K gate_up: the fused decode kernel takes only Q4_K, so 1 token is multi-kernel
+        kw["gate_up_type"] = "Q6_K"
     if variant == "topk1":
         kw["top_k"] = 1
     if variant == "few_experts":
@@ -180,22 +186,25 @@ def test_layer_variants(hip, variant):
     if variant == "inter_256_no_norm":
         lw["norm_topk_prob"] = False
     layer = hip.MoELayer.from_host(lw)
+    if variant == "q6k_gate_up":
+        assert layer.plan(1) == "gemv"
     for T in (1, 5):
         check_layer(hip, layer, lw, synth.tokens(51 + T, T, kw["hidden"]), f"{variant}")
 
 
 def check_prefill(hip, layer, lw, x, label, tol=TOL):
-    """The MFMA path against the oracle with the same bf16 roundings (x, dequantized weights, the SwiGLU output
-    and each expert's output to bf16, as the reference's bf16 F.linear path; fp32 products and sums), and against
-    the all-fp32 oracle within bf16 accuracy."""
-    print(f"[prefill] {label}: T={x.shape[0]}", flush=True)
+    """A plan with MFMA experts against the oracle's chain for that plan ("split": the reference's per-expert
+    rule; "mfma": every expert on the bf16 chain of engines/base.py:568-570 with bf16 tensors), and against the
+    all-fp32 oracle within bf16 accuracy."""
+    chain = {"split": "split", "mfma": "bf16"}[layer.plan(x.shape[0])]
+    print(f"[prefill] {label}: T={x.shape[0]} chain={chain}", flush=True)
     y, ids, wts = run_layer(hip, layer, x)
-    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, bf16_operands=True, bf16_outputs=True, return_routing=True)
+    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, chain=chain, return_routing=True)
     np.testing.assert_array_equal(ids, ids_ref)
     np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
     err = moe_ref.rel_err(y, y_b)
     err32 = moe_ref.rel_err(y, moe_ref.layer(x, lw))
-    print(f"[prefill] {label}: rel err {err:.2e} vs bf16-operand oracle, {err32:.2e} vs fp32 oracle", flush=True)
+    print(f"[prefill] {label}: rel err {err:.2e} vs the {chain} oracle, {err32:.2e} vs the fp32 oracle", flush=True)
     assert err < tol
     assert err32 < 2e-2
     return err
@@ -203,7 +212,7 @@ def check_prefill(hip, layer, lw, x, label, tol=TOL):
 
 def test_prefill_mfma_c2(hip, c2, layer_c2):
     """600 tokens through the full layer: tiled router, grouped bf16 MFMA GEMMs for ~19 tokens per expert."""
-    assert c2.plan(600) == "mfma"
+    assert c2.plan(600) == "split"
     check_prefill(hip, c2, layer_c2, synth.tokens(600, 600), "c2 T=600")
 
 
@@ -220,17 +229,20 @@ def test_prefill_full_chunk_sampled(hip, c2, layer_c2):
     np.testing.assert_array_equal(ids, ids_ref)
     np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
     pick = np.sort(np.random.default_rng(5).choice(T, 24, replace=False))
-    y_ref = moe_ref.layer(x[pick], layer_c2, bf16_operands=True, bf16_outputs=True)
+    counts = np.bincount(ids_ref.reshape(-1), minlength=layer_c2["experts"])
+    y_ref = moe_ref.layer(x[pick], layer_c2, chain="split", counts=counts, layer_tokens=T)
     err = moe_ref.rel_err(y[pick], y_ref)
     print(f"[prefill] full chunk T=4096, 24 sampled tokens: rel err {err:.2e}", flush=True)
     assert err < TOL
 
 
-@pytest.mark.parametrize("variant", ["base", "q4k_down", "no_shared", "inter_256", "partial_tiles"])
+@pytest.mark.parametrize("variant", ["base", "q4k_down", "q6k_gate_up", "no_shared", "inter_256", "partial_tiles"])
 def test_prefill_mfma_variants(hip, variant):
     kw = dict(hidden=1024, inter=512, shared_inter=512, experts=16, top_k=4)
     if variant == "q4k_down":
         kw["down_type"] = "Q4_K"
+    if variant == "q6k_gate_up":
+        kw["gate_up_type"] = "Q6_K"
     if variant == "inter_256":
         kw.update(inter=256, shared_inter=256)
     lw = synth.moe_layer(70, **kw)

@@ -40,7 +40,9 @@ struct ExpertArgs {
     const uint8_t* sh_down;
     const float* x;
     int T, H, inter, sh_inter, k;
-    int n_routed;  // grid slots [0, n_routed) are routed experts; slot n_routed (if launched) the shared expert
+    // work slots: the routed experts listed in active[1 .. active[0]] (when routed), then the shared expert over
+    // all T tokens (when shared_slot); a launch's workgroups loop over (slot, row group) items
+    int routed, shared_slot;
     const int32_t* offsets;
     const int32_t* active;
     const int32_t* sorted;
@@ -53,7 +55,11 @@ struct ExpertArgs {
 constexpr int kTileTokens = 144;             // prefill: tokens per gate_up GEMM tile (9 MFMA token tiles)
 constexpr int kDownTileTokens = 128;         // prefill: tokens per down GEMM tile (8 MFMA token tiles)
 constexpr int kDownSlabsMax = 4;            // prefill: most 256-row slabs per down workgroup
-constexpr int kGemvMaxTokens = 8;  // fp32 GEMV experts up to this many tokens, bf16 MFMA GEMMs above (gguf/metal.py:20)
+// An expert given at most this many tokens runs on the fp32 GEMV kernels with exact weights, one given more on the
+// bf16 MFMA GEMMs: the reference applies the rule of gguf/metal.py:20,404-407 to each expert's own tokens
+// (engines/base.py:566-571).
+constexpr int kGemvMaxTokens = 8;
+constexpr uint32_t kPosBf16 = 0x80000000u;  // pair_pos flag: the pair's expert output is bf16 (an MFMA expert)
 constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
 
 struct PrefillArgs {
@@ -71,7 +77,8 @@ struct PrefillArgs {
     const int32_t* n_tiles_down;
     uint16_t* h16;           // [T*k, inter] bf16 by sorted position
     uint16_t* h_sh16;        // [T, shared_inter] bf16
-    uint16_t* o16;           // [T*k, H] bf16 by sorted position (the reference's bf16 F.linear output)
+    uint16_t* o16;           // bf16 by sorted position, row pos at o16 + pos * ldo (the reference's bf16 F.linear output)
+    int64_t ldo;             // o16's row stride in values
     uint16_t* o_sh16;        // [T, H] bf16
     int H, inter, sh_inter, E, k;
     int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
@@ -112,11 +119,22 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T);
 int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,
                  hipStream_t s);
 int zero_sync(void* workspace, hipStream_t s);
+// How the routed experts of a T-token call are run: kPlanGemv (every expert on the fp32 GEMV kernels), kPlanSplit
+// (experts with more than kGemvMaxTokens tokens on the MFMA GEMMs, the rest on GEMV), kPlanMfma (every expert on
+// the MFMA GEMMs; WL_MOE_FORCE_MFMA). The fused single-kernel decode is chosen before this (fused_eligible).
+enum ExpertPlan { kPlanGemv = 0, kPlanSplit = 2, kPlanMfma = 3 };
+ExpertPlan expert_plan(const WlMoeLayer& L, int64_t T);
+// Whether the layer's shapes and types let the MFMA GEMMs run at T tokens.
 bool prefill_eligible(const WlMoeLayer& L, int64_t T);
-int max_tiles(const WlMoeLayer& L, int64_t T, int cap);
+// The most pairs an expert may have and still run on the GEMV kernels under `plan`.
+inline int plan_gemv_max(ExpertPlan plan) {
+    return plan == kPlanMfma ? 0 : plan == kPlanSplit ? kGemvMaxTokens : 0x7FFFFFFF;
+}
+int max_tiles(const WlMoeLayer& L, int64_t T, int cap, int gemv_max);
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s);
-int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s);
+int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);
+int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);
 int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x, int64_t T, uint16_t* y,
                   hipStream_t s);
 

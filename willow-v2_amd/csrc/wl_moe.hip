@@ -210,12 +210,15 @@ __device__ __forceinline__ int chunk_rank(const uint32_t* bits, int e, int t) {
     return r;
 }
 
-// With tiles non-null (the MFMA path), the sort's single-workgroup stage also writes the GEMMs' tile lists.
+// With tiles non-null (an MFMA plan), the sort's single-workgroup stage also writes the GEMMs' tile lists, for the
+// experts with more than gemv_max pairs (and the shared expert); `active` then lists only the others (the GEMV
+// experts), and pair_pos flags the pairs of MFMA experts with kPosBf16.
 struct TileOut {
     int4* tiles;
     int4* tiles_down;
     int32_t* n_tiles;
     int with_shared;
+    int gemv_max;
 };
 
 __global__ __launch_bounds__(1024) void k_sort_hist(const int32_t* __restrict__ ids, int T, int k, int E,
@@ -237,9 +240,11 @@ __global__ __launch_bounds__(1024) void k_sort_hist(const int32_t* __restrict__ 
     }
 }
 
+// flag_above: pairs of experts with more than this many pairs get kPosBf16 in pair_pos (the MFMA experts)
 __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int T, int k, int E,
                                                       const int32_t* __restrict__ rank,
                                                       const int32_t* __restrict__ hist,
+                                                      const int32_t* __restrict__ offsets, int flag_above,
                                                       int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= static_cast<int64_t>(T) * k) return;
@@ -247,8 +252,9 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
     if (e < 0 || e >= E) return;
     const int c = static_cast<int>(p / k) / kSortChunk;
     const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
+    const bool bf16 = offsets[e + 1] - offsets[e] > flag_above;
     sorted[pos] = static_cast<int32_t>(p);
-    pair_pos[p] = pos;
+    pair_pos[p] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (bf16 ? kPosBf16 : 0u));
 }
 
 // One chunk (T <= kSortChunk), a workgroup of 1024 threads: one thread per expert builds the stable counting sort
@@ -284,9 +290,10 @@ __device__ int block_scan_excl(int v, int* wsum, int* total) {
     return r;
 }
 
-// GEMM tiles: each routed expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles
+// GEMM tiles: each MFMA expert's sorted positions, then the shared expert's tokens (expert id E), cut into tiles
 // of at most `cap` tokens; tiles[i] = (expert, first position or token, count, 0), n_tiles[0] = how many. Thread e
-// holds expert e's count c and first position off; every thread of the workgroup takes part (E <= blockDim.x).
+// holds expert e's count c (0 for an expert left to the GEMV kernels) and first position off; every thread of the
+// workgroup takes part (E <= blockDim.x).
 __device__ void tile_list(int4* __restrict__ tiles, int32_t* __restrict__ n_tiles, int cap, int e, int E,
                                 int c, int off, int T, int with_shared, int* wsum) {
     int total;
@@ -306,7 +313,7 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
                                                                   int32_t* __restrict__ pair_pos, TileOut to) {
     __shared__ int32_t lds_ids[kSortChunk * WL_MAX_TOPK];
     __shared__ uint32_t bits[kSortWords * 64 * kMaxEJ];  // expert e: words kSortWords e .. + kSortWords - 1
-    __shared__ int32_t lds_off[64 * kMaxEJ];
+    __shared__ uint32_t lds_off[64 * kMaxEJ];  // first sorted position | kPosBf16 for an MFMA expert
     __shared__ int wsum[kSortSmallThreads / 64];
     const int tid = threadIdx.x;
     const int P = T * k;
@@ -325,24 +332,26 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
         for (int wd = 0; wd < kSortWords; wd++) c += __popc(bits[kSortWords * e + wd]);
     int total;
     const int off = block_scan_excl(c, wsum, &total);
+    const bool big = to.tiles && c > to.gemv_max;  // an MFMA expert
     if (e < E) {
         offsets[e] = off;
-        lds_off[e] = off;
+        lds_off[e] = static_cast<uint32_t>(off) | (big ? kPosBf16 : 0u);
     }
     if (tid == 0) offsets[E] = P;
-    const int apos = block_scan_excl(c > 0 ? 1 : 0, wsum, &total);  // its barriers also publish lds_off
-    if (e < E && c > 0) active[1 + apos] = e;
+    const int apos = block_scan_excl((c > 0 && !big) ? 1 : 0, wsum, &total);  // its barriers also publish lds_off
+    if (e < E && c > 0 && !big) active[1 + apos] = e;
     if (tid == 0) active[0] = total;
     for (int q = tid; q < P; q += blockDim.x) {
         const int ex = lds_ids[q];
         if (ex < 0 || ex >= E) continue;
-        const int pos = lds_off[ex] + chunk_rank(bits, ex, q / k);
+        const uint32_t o = lds_off[ex];
+        const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
         sorted[pos] = q;
-        pair_pos[q] = pos;
+        pair_pos[q] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (o & kPosBf16));
     }
     if (to.tiles) {
-        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
-        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
+        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
     }
 }
 
@@ -393,19 +402,22 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_scan(int T, int k, i
             }
         }
     }
-    const int apos = block_scan_excl(c > 0 ? 1 : 0, wsum, &total);
-    if (mine && c > 0) active[1 + apos] = e;
+    const bool big = to.tiles && c > to.gemv_max;  // an MFMA expert
+    const int apos = block_scan_excl((c > 0 && !big) ? 1 : 0, wsum, &total);
+    if (mine && c > 0 && !big) active[1 + apos] = e;
     if (threadIdx.x == 0) active[0] = total;
     if (to.tiles) {
-        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, c, off, T, to.with_shared, wsum);
-        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, c, off, T, to.with_shared, wsum);
+        tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
+        tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
     }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Experts. grid.y = expert slot: slots [0, n_routed) are active experts (active[1 + slot]); slot n_routed, when
-// with_shared, is the shared expert over all T tokens. Outputs are indexed by sorted position (routed) or token
-// (shared).
+// Experts on the fp32 GEMV kernels. A launch's work slots are the routed experts listed in active[1 ..
+// active[0]] (when a.routed) and then the shared expert over all T tokens (when a.shared_slot); each slot's rows
+// are cut into row groups of one workgroup each, and the workgroups loop over the (slot, row group) items, so the
+// grid can be sized for the most experts a call may have while only the listed ones cost anything. Outputs are
+// indexed by sorted position (routed) or token (shared).
 struct ExpertView {
     const uint8_t* w;
     int64_t stride_rows;  // offset of the up half (gate_up) in rows
@@ -413,9 +425,14 @@ struct ExpertView {
     bool routed;
 };
 
-__device__ __forceinline__ bool expert_view(const ExpertArgs& a, int slot, bool up_proj, ExpertView& v) {
-    if (slot < a.n_routed) {
-        if (slot >= a.active[0]) return false;
+__device__ __forceinline__ int expert_slots(const ExpertArgs& a) {
+    return (a.routed ? a.active[0] : 0) + a.shared_slot;
+}
+
+__device__ __forceinline__ ExpertView expert_view(const ExpertArgs& a, int slot, bool up_proj) {
+    ExpertView v;
+    const int n_routed = a.routed ? a.active[0] : 0;
+    if (slot < n_routed) {
         const int e = a.active[1 + slot];
         v.w = (up_proj ? a.gate_up : a.down) + static_cast<int64_t>(e) * (up_proj ? a.gate_up_stride : a.down_stride);
         v.stride_rows = a.inter;
@@ -429,121 +446,197 @@ __device__ __forceinline__ bool expert_view(const ExpertArgs& a, int slot, bool 
         v.end = a.T;
         v.routed = false;
     }
-    return true;
+    return v;
 }
 
-// gate_up + SwiGLU: wave = one intermediate row j (gate row j and up row inter + j); lanes split the hidden dim
-// into blocks (group g -> blocks g, g+8, ...). h[pos, j] = silu(gate . x_t) * (up . x_t).
-template <int TYPE, int TT>
-__global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a) {
-    ExpertView v;
-    if (!expert_view(a, blockIdx.y, true, v)) return;
-    const int inter = static_cast<int>(v.stride_rows);
-    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (j >= inter) return;
-    if constexpr (TT == 1) {  // one token per expert: the shared gate_up_row, as the fused decode kernel
-        const int lane1 = threadIdx.x & 63;
-        for (int pos = v.begin; pos < v.end; pos++) {
-            const int tok = v.routed ? a.sorted[pos] / a.k : pos;
-            float gs, us;
-            gate_up_row<TYPE>(v.w, j, inter, a.H, a.x + static_cast<int64_t>(tok) * a.H, lane1, gs, us);
-            if (lane1 == 0) (v.routed ? a.h : a.h_sh)[static_cast<int64_t>(v.routed ? pos : tok) * inter + j] =
-                silu(gs) * us;
-        }
-        return;
+// Both GEMV expert kernels handle an expert's tokens kGemvTok at a time: the workgroup first copies those tokens'
+// activation rows (x for gate_up, h for down) into LDS, all loads in flight at once, so their latency is paid once
+// per chunk, not once per token. In LDS a row of `width` values is padded by 4 floats after every 64 (lds_index),
+// which spreads the lanes' 16-byte reads over the banks. Then each wavefront decodes the weight blocks of several
+// rows once and runs every token of the chunk through them, reading the activations from LDS.
+constexpr int kGemvTok = 8;        // tokens per LDS chunk (an expert on the GEMV kernels has at most 8 in a split plan)
+constexpr int kGuRows = 4;         // gate_up: intermediate rows (a gate row and its up row) per wavefront
+constexpr int kDnPasses = 4;       // down: row passes per wavefront (R rows each)
+constexpr int kGemvLdsMax = 80 << 10;
+
+__host__ __device__ inline int lds_row_floats(int width) { return width + 4 * (width / 64); }
+__device__ __forceinline__ int lds_index(int i) { return i + 4 * (i >> 6); }
+
+// Tokens per chunk for rows of `width` values: kGemvTok, or fewer when their LDS copy would pass kGemvLdsMax.
+__host__ inline int gemv_chunk(int width) {
+    const int per = kGemvLdsMax / (4 * lds_row_floats(width));
+    return per < 1 ? 1 : (per < kGemvTok ? per : kGemvTok);
+}
+
+// rows u < n of the chunk: src_row(u) -> LDS row u (width values, a multiple of 64), 16 bytes per load
+template <typename SrcRow>
+__device__ __forceinline__ void stage_rows(float* lds, int n, int width, SrcRow src_row) {
+    const int per_row = width / 4;
+    const int ld = lds_row_floats(width);
+    for (int f = threadIdx.x; f < n * per_row; f += blockDim.x) {
+        const int u = f / per_row, i = 4 * (f - u * per_row);
+        *reinterpret_cast<float4*>(lds + u * ld + lds_index(i)) =
+            *reinterpret_cast<const float4*>(src_row(u) + i);
     }
+}
+
+// the lane's 16 values from LDS row u at value offset i (16-aligned: never straddles a padding gap)
+__device__ __forceinline__ void lds_run(const float* lds, int ld, int u, int i, float4 x[4]) {
+    const float4* q = reinterpret_cast<const float4*>(lds + u * ld + lds_index(i));
+#pragma unroll
+    for (int j = 0; j < 4; j++) x[j] = q[j];
+}
+
+// gate_up + SwiGLU: a row group is 4 kGuRows intermediate rows; wavefront w takes rows j0 .. j0 + kGuRows - 1
+// (gate rows j, up rows inter + j); lane group g takes blocks g, g + 8, ... of each row. With at most 8 blocks per
+// row (hidden <= 2048) a lane holds one block of each of its rows, decoded once for all the chunk's tokens; wider
+// rows are decoded again per token. h[pos, j] = silu(gate . x_t) * (up . x_t). rows: the intermediate width of
+// every slot of the launch.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a, int rows, int chunk) {
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
+    constexpr int kRowsPerGroup = 4 * kGuRows;
+    const int groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+    const int items = expert_slots(a) * groups;
     const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
-    const uint8_t* wg = v.w + static_cast<int64_t>(j) * rs;
-    const uint8_t* wu = v.w + static_cast<int64_t>(inter + j) * rs;
     const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
-    float* hout = v.routed ? a.h : a.h_sh;
-    for (int p0 = v.begin; p0 < v.end; p0 += TT) {
-        int tok[TT];
+    const int ld = lds_row_floats(a.H);
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int slot = it / groups;
+        const ExpertView v = expert_view(a, slot, true);
+        const int inter = static_cast<int>(v.stride_rows);
+        const int j0 = (it - slot * groups) * kRowsPerGroup + wv * kGuRows;
+        float* hout = v.routed ? a.h : a.h_sh;
+        // the lane's weights of block kb for the wavefront's rows (rows past inter load row inter - 1, never stored)
+        Lane32 wg[kGuRows], wu[kGuRows];
+        auto decode_rows = [&](int kb) {
+            RawLane<TYPE> rg[kGuRows], ru[kGuRows];
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            const int pos = p0 + u;
-            tok[u] = pos < v.end ? (v.routed ? a.sorted[pos] / a.k : pos) : -1;
-        }
-        float ag[TT], au[TT];
-#pragma unroll
-        for (int u = 0; u < TT; u++) ag[u] = au[u] = 0.0f;
-        for (int kb = g; kb < nb; kb += 8) {
-            Lane32 lg, lu;
-            decode<TYPE>(wg + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lg);
-            decode<TYPE>(wu + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, lu);
-#pragma unroll
-            for (int u = 0; u < TT; u++) {
-                if (tok[u] >= 0) {
-                    const float* xt = a.x + static_cast<int64_t>(tok[u]) * a.H + kb * kQK + lo_start;
-                    float4 xl[4], xh[4];
-                    load_run(xt, xl);
-                    load_run(xt + hi_off, xh);
-                    const float sxl = sum16(xl), sxh = sum16(xh);
-                    ag[u] += lane_dot_s(lg, xl, xh, sxl, sxh);
-                    au[u] += lane_dot_s(lu, xl, xh, sxl, sxh);
-                }
+            for (int r = 0; r < kGuRows; r++) {
+                const int j = min(j0 + r, inter - 1);
+                rg[r].fetch(v.w + static_cast<int64_t>(j) * rs + kb * BlockInfo<TYPE>::bytes, c);
+                ru[r].fetch(v.w + static_cast<int64_t>(inter + j) * rs + kb * BlockInfo<TYPE>::bytes, c);
             }
-        }
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            const float gs = group_sum<64>(ag[u]);
-            const float us = group_sum<64>(au[u]);
-            if (lane == 0 && tok[u] >= 0) {
-                const int64_t row = v.routed ? p0 + u : tok[u];
-                hout[row * inter + j] = silu(gs) * us;
+            for (int r = 0; r < kGuRows; r++) {
+                rg[r].unpack(c, wg[r]);
+                ru[r].unpack(c, wu[r]);
+            }
+        };
+        const bool one_block = nb <= 8;
+        if (one_block && g < nb && j0 < inter) decode_rows(g);  // issued before the x staging waits
+        for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
+            const int n = min(chunk, v.end - p0);
+            __syncthreads();  // the previous chunk's LDS rows are no longer read
+            stage_rows(lds_x, n, a.H, [&](int u) {
+                const int pos = p0 + u;
+                return a.x + static_cast<int64_t>(v.routed ? a.sorted[pos] / a.k : pos) * a.H;
+            });
+            __syncthreads();
+            if (j0 >= inter) continue;  // whole wavefront (it still takes part in the barriers)
+#pragma unroll 1
+            for (int u = 0; u < n; u++) {
+                float ag[kGuRows], au[kGuRows];
+#pragma unroll
+                for (int r = 0; r < kGuRows; r++) ag[r] = au[r] = 0.0f;
+                for (int kb = g; kb < nb; kb += 8) {
+                    if (!one_block) decode_rows(kb);
+                    float4 xl[4], xh[4];
+                    lds_run(lds_x, ld, u, kb * kQK + lo_start, xl);
+                    lds_run(lds_x, ld, u, kb * kQK + lo_start + hi_off, xh);
+                    const float sxl = sum16(xl), sxh = sum16(xh);
+#pragma unroll
+                    for (int r = 0; r < kGuRows; r++) {
+                        ag[r] += lane_dot_s(wg[r], xl, xh, sxl, sxh);
+                        au[r] += lane_dot_s(wu[r], xl, xh, sxl, sxh);
+                    }
+                }
+                const int64_t row = p0 + u;  // routed: sorted position; shared: token
+#pragma unroll
+                for (int r = 0; r < kGuRows; r++) {
+                    const float gs = group_sum<64>(ag[r]);
+                    const float us = group_sum<64>(au[r]);
+                    if (lane == 0 && j0 + r < inter) hout[row * inter + j0 + r] = silu(gs) * us;
+                }
             }
         }
     }
 }
 
-// down: wave = R output rows (nb = inter/256 blocks each; see row_geom); o[pos, r] = down[r] . h[pos].
-template <int TYPE, int TT, int WIDTH>
-__global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
-    ExpertView v;
-    if (!expert_view(a, blockIdx.y, false, v)) return;
+// down: a row group is 4 wavefronts x kDnPasses passes x R output rows (R = 64 / WIDTH, WIDTH = 8 nb lanes per
+// row when nb = inter / 256 is 1, 2 or 4: the lane then holds one block of each of its rows, decoded once; otherwise
+// one row per pass over all 64 lanes, blocks g, g + 8, ..., decoded again per token). o[pos, r] = down[r] . h[pos];
+// a lane's h runs are the same for every row it covers, so each token's are read from LDS once per block.
+template <int TYPE, int WIDTH>
+__global__ __launch_bounds__(256) void k_down(ExpertArgs a, int chunk) {
+    extern __shared__ __attribute__((aligned(16))) float lds_h[];
     constexpr int R = WIDTH == 64 ? 1 : 64 / WIDTH;
-    const int inter = static_cast<int>(v.stride_rows);
-    const int nb = inter / kQK;
-    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    constexpr int kRowsPerWave = R * kDnPasses;
+    const int groups = (a.H + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
+    const int items = expert_slots(a) * groups;
     const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
-    const int row_off = R > 1 ? g / nb : 0;
-    const int kb0 = R > 1 ? g % nb : g;
-    const int kb_step = R > 1 ? nb : 8;
-    const bool slot_used = R > 1 ? (g < R * nb) : true;
-    const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R + row_off;
-    if ((blockIdx.x * 4 + (threadIdx.x >> 6)) * R >= a.H) return;  // whole wave
-    const bool row_ok = slot_used && row < a.H;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
-    const uint8_t* wr = v.w + static_cast<int64_t>(row_ok ? row : 0) * rs;
-    const float* hin = v.routed ? a.h : a.h_sh;
-    float* oout = v.routed ? a.o : a.o_sh;
-    for (int p0 = v.begin; p0 < v.end; p0 += TT) {
-        float acc[TT];
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int slot = it / groups;
+        const ExpertView v = expert_view(a, slot, false);
+        const int inter = static_cast<int>(v.stride_rows);
+        const int nb = inter / kQK;
+        const int ld = lds_row_floats(inter);
+        const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+        const int row_off = R > 1 ? g / nb : 0;
+        const int kb0 = R > 1 ? g % nb : g;
+        const int kb_step = R > 1 ? nb : 8;
+        const bool slot_used = R > 1 ? (g < R * nb) : true;
+        const int wave_row0 = (it - slot * groups) * 4 * kRowsPerWave + wv * kRowsPerWave;
+        const float* hin = v.routed ? a.h : a.h_sh;
+        float* oout = v.routed ? a.o : a.o_sh;
+        Lane32 w[kDnPasses];
+        auto decode_rows = [&](int kb) {
+            RawLane<TYPE> raw[kDnPasses];
 #pragma unroll
-        for (int u = 0; u < TT; u++) acc[u] = 0.0f;
-        if (row_ok) {
-            for (int kb = kb0; kb < nb; kb += kb_step) {
-                Lane32 l;
-                decode<TYPE>(wr + static_cast<int64_t>(kb) * BlockInfo<TYPE>::bytes, c, l);
+            for (int q = 0; q < kDnPasses; q++) {
+                const int row = min(wave_row0 + q * R + row_off, a.H - 1);  // past H: never stored
+                raw[q].fetch(v.w + static_cast<int64_t>(row) * rs + kb * BlockInfo<TYPE>::bytes, c);
+            }
 #pragma unroll
-                for (int u = 0; u < TT; u++) {
-                    if (p0 + u < v.end) {
-                        const float* hp = hin + static_cast<int64_t>(p0 + u) * inter + kb * kQK + lo_start;
+            for (int q = 0; q < kDnPasses; q++) raw[q].unpack(c, w[q]);
+        };
+        const bool one_block = R > 1;  // the lane's only block is kb0
+        if (one_block && slot_used && wave_row0 < a.H) decode_rows(kb0);
+        for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
+            const int n = min(chunk, v.end - p0);
+            __syncthreads();
+            stage_rows(lds_h, n, inter, [&](int u) { return hin + static_cast<int64_t>(p0 + u) * inter; });
+            __syncthreads();
+            if (wave_row0 >= a.H) continue;  // whole wavefront
+#pragma unroll 1
+            for (int u = 0; u < n; u++) {
+                float acc[kDnPasses];
+#pragma unroll
+                for (int q = 0; q < kDnPasses; q++) acc[q] = 0.0f;
+                if (slot_used) {
+                    for (int kb = kb0; kb < nb; kb += kb_step) {
+                        if (!one_block) decode_rows(kb);
                         float4 xl[4], xh[4];
-                        load_run(hp, xl);
-                        load_run(hp + hi_off, xh);
-                        acc[u] += lane_dot(l, xl, xh);
+                        lds_run(lds_h, ld, u, kb * kQK + lo_start, xl);
+                        lds_run(lds_h, ld, u, kb * kQK + lo_start + hi_off, xh);
+                        const float sxl = sum16(xl), sxh = sum16(xh);
+#pragma unroll
+                        for (int q = 0; q < kDnPasses; q++) acc[q] += lane_dot_s(w[q], xl, xh, sxl, sxh);
                     }
                 }
-            }
-        }
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            const float s = group_sum<WIDTH>(acc[u]);
-            if ((lane & (WIDTH - 1)) == 0 && row_ok && p0 + u < v.end)
-                oout[static_cast<int64_t>(p0 + u) * a.H + row] = s;
+                for (int q = 0; q < kDnPasses; q++) {
+                    const float sum = group_sum<WIDTH>(acc[q]);
+                    const int row = wave_row0 + q * R + row_off;
+                    if ((lane & (WIDTH - 1)) == 0 && slot_used && row < a.H)
+                        oout[static_cast<int64_t>(p0 + u) * a.H + row] = sum;
+                }
+            }
         }
     }
 }
@@ -552,7 +645,9 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a) {
 // takes kCombineSpan values of one token, 8 per thread, so the token's routing (indices and weights, the same for
 // the whole workgroup) is read with scalar loads once per workgroup. For k <= 8 every index and weight is loaded
 // first and then every o row, so the loads overlap instead of forming k dependent chains; the sum is the same in
-// both forms. OT: float (GEMV path) or uint16_t (bf16, MFMA path). H is a multiple of 8.
+// both forms. Position pos's output row starts at byte 4 H pos of o: fp32 from a GEMV expert, or bf16 (its first
+// 2 H bytes) from an MFMA expert, which pair_pos marks with kPosBf16. SH: the shared expert's output type (float or
+// uint16_t for bf16, rows of H). H is a multiple of 8.
 constexpr int kCombineUnroll = 8;
 constexpr int kCombineSpan = 8 * 256;
 
@@ -570,12 +665,16 @@ __device__ __forceinline__ Float8 load8(const uint16_t* p) {
     const uint4 v = *reinterpret_cast<const uint4*>(p);
     return {bf16x4_to_float4(v.x, v.y), bf16x4_to_float4(v.z, v.w)};
 }
+// 8 values of position pos's output row, from column r (flag: the row is bf16)
+__device__ __forceinline__ Float8 load_o8(const float* o, int64_t pos, int H, int r, bool bf16) {
+    return bf16 ? load8(reinterpret_cast<const uint16_t*>(o) + pos * 2 * H + r) : load8(o + pos * H + r);
+}
 
-template <typename OT>
+template <typename SH>
 __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int32_t* __restrict__ corder,
                                                  const int32_t* __restrict__ pair_pos,
-                                                 const float* __restrict__ wts, const OT* __restrict__ o,
-                                                 const OT* __restrict__ o_sh, const float* __restrict__ sg,
+                                                 const float* __restrict__ wts, const float* __restrict__ o,
+                                                 const SH* __restrict__ o_sh, const float* __restrict__ sg,
                                                  float* __restrict__ y) {
     const int spans = (H + kCombineSpan - 1) / kCombineSpan;
     const int t = static_cast<int>(blockIdx.x) / spans;
@@ -599,33 +698,42 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             a1.w += wv * ov.b.w;
         }
     };
+    // a pair's position (-1 when out of range: never for ids from k_topk; guards caller-supplied ids) and flag
+    auto position = [&](int64_t q, bool& bf16) {
+        const uint32_t pp = static_cast<uint32_t>(pair_pos[q]);
+        bf16 = (pp & kPosBf16) != 0;
+        const int pos = static_cast<int>(pp & ~kPosBf16);
+        return pos < P ? pos : -1;
+    };
     if (k <= kCombineUnroll) {
         int pos[kCombineUnroll];
+        bool bf[kCombineUnroll];
         float wv[kCombineUnroll];
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++) {
             pos[n] = -1;
+            bf[n] = false;
             wv[n] = 0.0f;
             if (n < k) {
                 const int64_t q = base + corder[base + n];
-                pos[n] = pair_pos[q];
+                pos[n] = position(q, bf[n]);
                 wv[n] = wts[q];
             }
         }
         Float8 ov[kCombineUnroll];
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
-            if (n < k && pos[n] >= 0 && pos[n] < P)  // never false for ids from k_topk; guards caller-supplied ids
-                ov[n] = load8(o + static_cast<int64_t>(pos[n]) * H + r);
+            if (n < k && pos[n] >= 0) ov[n] = load_o8(o, pos[n], H, r, bf[n]);
 #pragma unroll
         for (int n = 0; n < kCombineUnroll; n++)
-            if (n < k && pos[n] >= 0 && pos[n] < P) add(n, wv[n], ov[n]);
+            if (n < k && pos[n] >= 0) add(n, wv[n], ov[n]);
     } else {
         for (int n = 0; n < k; n++) {
             const int64_t q = base + corder[base + n];
-            const int pos = pair_pos[q];
-            if (pos < 0 || pos >= P) continue;
-            add(n, wts[q], load8(o + static_cast<int64_t>(pos) * H + r));
+            bool bf16;
+            const int pos = position(q, bf16);
+            if (pos < 0) continue;
+            add(n, wts[q], load_o8(o, pos, H, r, bf16));
         }
     }
     if (o_sh) {
@@ -678,10 +786,12 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.o = static_cast<float*>(take(sizeof(float) * P * L.hidden));
     w.h_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.shared_inter : 0));
     w.o_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.hidden : 0));
-    const bool mfma = prefill_eligible(L, T);
+    const ExpertPlan plan = expert_plan(L, T);
+    const bool mfma = plan != kPlanGemv;
+    const int gmax = plan_gemv_max(plan);
     w.xb = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * T * L.hidden : 0));
-    w.tiles = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kTileTokens) : 0));
-    w.tiles_down = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kDownTileTokens) : 0));
+    w.tiles = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kTileTokens, gmax) : 0));
+    w.tiles_down = static_cast<int4*>(take(mfma ? sizeof(int4) * max_tiles(L, T, kDownTileTokens, gmax) : 0));
     w.n_tiles = static_cast<int32_t*>(take(mfma ? 2 * sizeof(int32_t) : 0));
     w.h16 = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * P * L.inter : 0));
     w.h_sh16 = static_cast<uint16_t*>(take(mfma && shared ? sizeof(uint16_t) * T * L.shared_inter : 0));
@@ -750,10 +860,11 @@ static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int3
     return launch_status();
 }
 
+// The grouping; with an MFMA plan (tiles) also the tile lists of the experts with more than gemv_max pairs.
 static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* ids, int64_t T, bool tiles,
-                       hipStream_t s) {
+                       int gemv_max, hipStream_t s) {
     const int E = L.n_experts, k = L.top_k;
-    const TileOut to{tiles ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0};
+    const TileOut to{tiles ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0, gemv_max};
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
     if (nchunks == 1) {
         k_sort_small<<<1, kSortSmallThreads, 0, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted,
@@ -764,60 +875,64 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
         k_sort_scan<<<1, kSortSmallThreads, 0, s>>>(static_cast<int>(T), k, E, nchunks, w.hist, w.offsets,
                                                     w.active, to);
         const int64_t P = T * k;
-        k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(ids, static_cast<int>(T), k, E, w.rank,
-                                                                          w.hist, w.sorted, w.pair_pos);
+        k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(
+            ids, static_cast<int>(T), k, E, w.rank, w.hist, w.offsets, tiles ? gemv_max : 0x7FFFFFFF, w.sorted,
+            w.pair_pos);
     }
     return launch_status();
 }
 
-template <int TYPE>
-static void launch_gate_up_t(const ExpertArgs& a, int rows, int slots, hipStream_t s) {
-    const dim3 grid((rows + 3) / 4, slots);
-    if (a.T == 1)
-        k_gate_up<TYPE, 1><<<grid, 256, 0, s>>>(a);
-    else
-        k_gate_up<TYPE, 4><<<grid, 256, 0, s>>>(a);
+// Workgroups of a GEMV expert launch: enough to fill the GPU several times over, never more than the items
+static unsigned gemv_grid(int64_t items) {
+    constexpr int64_t kMaxGroups = 2048;
+    return static_cast<unsigned>(items < kMaxGroups ? (items > 0 ? items : 1) : kMaxGroups);
 }
 
-static void launch_gate_up(int type, const ExpertArgs& a, int rows, int slots, hipStream_t s) {
+template <int TYPE>
+static void launch_gate_up_t(const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
+    const unsigned grid = gemv_grid(static_cast<int64_t>(max_slots) * ((rows + 4 * kGuRows - 1) / (4 * kGuRows)));
+    const int chunk = gemv_chunk(a.H);
+    k_gate_up<TYPE><<<grid, 256, sizeof(float) * chunk * lds_row_floats(a.H), s>>>(a, rows, chunk);
+}
+
+static void launch_gate_up(int type, const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
     if (type == WL_TYPE_Q4_K)
-        launch_gate_up_t<WL_TYPE_Q4_K>(a, rows, slots, s);
+        launch_gate_up_t<WL_TYPE_Q4_K>(a, rows, max_slots, s);
     else
-        launch_gate_up_t<WL_TYPE_Q6_K>(a, rows, slots, s);
+        launch_gate_up_t<WL_TYPE_Q6_K>(a, rows, max_slots, s);
 }
 
 template <int TYPE, int WIDTH>
-static void launch_down_w(const ExpertArgs& a, int slots, hipStream_t s) {
+static void launch_down_w(const ExpertArgs& a, int inter, int max_slots, hipStream_t s) {
     constexpr int R = WIDTH == 64 ? 1 : 64 / WIDTH;
-    const dim3 grid((a.H + 4 * R - 1) / (4 * R), slots);
-    if (a.T == 1)
-        k_down<TYPE, 1, WIDTH><<<grid, 256, 0, s>>>(a);
-    else
-        k_down<TYPE, 4, WIDTH><<<grid, 256, 0, s>>>(a);
+    const unsigned grid =
+        gemv_grid(static_cast<int64_t>(max_slots) * ((a.H + 4 * R * kDnPasses - 1) / (4 * R * kDnPasses)));
+    const int chunk = gemv_chunk(inter);
+    k_down<TYPE, WIDTH><<<grid, 256, sizeof(float) * chunk * lds_row_floats(inter), s>>>(a, chunk);
 }
 
 template <int TYPE>
-static void launch_down_t(const ExpertArgs& a, int inter, int slots, hipStream_t s) {
+static void launch_down_t(const ExpertArgs& a, int inter, int max_slots, hipStream_t s) {
     switch (row_geom_width(inter / kQK)) {
-        case 8: launch_down_w<TYPE, 8>(a, slots, s); break;
-        case 16: launch_down_w<TYPE, 16>(a, slots, s); break;
-        case 32: launch_down_w<TYPE, 32>(a, slots, s); break;
-        default: launch_down_w<TYPE, 64>(a, slots, s); break;
+        case 8: launch_down_w<TYPE, 8>(a, inter, max_slots, s); break;
+        case 16: launch_down_w<TYPE, 16>(a, inter, max_slots, s); break;
+        case 32: launch_down_w<TYPE, 32>(a, inter, max_slots, s); break;
+        default: launch_down_w<TYPE, 64>(a, inter, max_slots, s); break;
     }
 }
 
-static void launch_down(int type, const ExpertArgs& a, int inter, int slots, hipStream_t s) {
+static void launch_down(int type, const ExpertArgs& a, int inter, int max_slots, hipStream_t s) {
     if (type == WL_TYPE_Q4_K)
-        launch_down_t<WL_TYPE_Q4_K>(a, inter, slots, s);
+        launch_down_t<WL_TYPE_Q4_K>(a, inter, max_slots, s);
     else
-        launch_down_t<WL_TYPE_Q6_K>(a, inter, slots, s);
+        launch_down_t<WL_TYPE_Q6_K>(a, inter, max_slots, s);
 }
 
-// The fp32 expert stages (gate_up + SwiGLU, down) for few tokens per expert.
-template <typename Mark>
-static int launch_gemv_experts(const WlMoeLayer& L, const float* x, int64_t tokens, const Workspace& w,
-                               hipStream_t s, Mark mark) {
-    const bool shared = L.shared_gate_up != nullptr;
+// The fp32 GEMV expert stages (gate_up + SwiGLU, then down) of the experts listed in `active`, and of the shared
+// expert when with_shared. max_routed bounds how many experts the list can hold (it sizes the grids; the kernels
+// read the actual count).
+static ExpertArgs gemv_args(const WlMoeLayer& L, const float* x, int64_t tokens, const Workspace& w, int max_routed,
+                            bool with_shared) {
     ExpertArgs a{};
     a.gate_up = static_cast<const uint8_t*>(L.gate_up);
     a.gate_up_stride = L.gate_up_stride;
@@ -829,7 +944,7 @@ static int launch_gemv_experts(const WlMoeLayer& L, const float* x, int64_t toke
     a.T = static_cast<int>(tokens);
     a.H = L.hidden;
     a.inter = L.inter;
-    a.sh_inter = shared ? L.shared_inter : 0;
+    a.sh_inter = with_shared ? L.shared_inter : 0;
     a.k = L.top_k;
     a.offsets = w.offsets;
     a.active = w.active;
@@ -838,26 +953,39 @@ static int launch_gemv_experts(const WlMoeLayer& L, const float* x, int64_t toke
     a.h_sh = w.h_sh;
     a.o = w.o;
     a.o_sh = w.o_sh;
-    const int max_active = static_cast<int>(tokens * L.top_k < L.n_experts ? tokens * L.top_k : L.n_experts);
+    a.routed = max_routed > 0 ? 1 : 0;
+    return a;
+}
 
-    // gate_up + SwiGLU: routed experts, then (same kernel when the types agree) the shared expert
-    const bool fuse_gu = shared && L.shared_gate_up_type == L.gate_up_type && L.shared_inter == L.inter;
-    a.n_routed = max_active;
-    launch_gate_up(L.gate_up_type, a, L.inter, max_active + (fuse_gu ? 1 : 0), s);
-    if (shared && !fuse_gu) {
-        ExpertArgs b = a;
-        b.n_routed = 0;
-        launch_gate_up(L.shared_gate_up_type, b, L.shared_inter, 1, s);
+static void launch_gemv_gate_up(const WlMoeLayer& L, ExpertArgs a, int max_routed, bool with_shared,
+                                hipStream_t s) {
+    // the routed experts and the shared expert share a launch when their types and widths agree
+    const bool fuse = with_shared && L.shared_gate_up_type == L.gate_up_type && L.shared_inter == L.inter;
+    a.shared_slot = fuse ? 1 : 0;
+    if (max_routed > 0 || fuse) launch_gate_up(L.gate_up_type, a, L.inter, max_routed + a.shared_slot, s);
+    if (with_shared && !fuse) {
+        a.routed = 0;
+        a.shared_slot = 1;
+        launch_gate_up(L.shared_gate_up_type, a, L.shared_inter, 1, s);
     }
-    const bool fuse_dn = shared && L.shared_down_type == L.down_type && L.shared_inter == L.inter;
-    mark(4);
-    launch_down(L.down_type, a, L.inter, max_active + (fuse_dn ? 1 : 0), s);
-    if (shared && !fuse_dn) {
-        ExpertArgs b = a;
-        b.n_routed = 0;
-        launch_down(L.shared_down_type, b, L.shared_inter, 1, s);
+}
+
+static void launch_gemv_down(const WlMoeLayer& L, ExpertArgs a, int max_routed, bool with_shared, hipStream_t s) {
+    const bool fuse = with_shared && L.shared_down_type == L.down_type && L.shared_inter == L.inter;
+    a.shared_slot = fuse ? 1 : 0;
+    if (max_routed > 0 || fuse) launch_down(L.down_type, a, L.inter, max_routed + a.shared_slot, s);
+    if (with_shared && !fuse) {
+        a.routed = 0;
+        a.shared_slot = 1;
+        launch_down(L.shared_down_type, a, L.shared_inter, 1, s);
     }
-    return launch_status();
+}
+
+ExpertPlan expert_plan(const WlMoeLayer& L, int64_t T) {
+    if (L.flags & WL_MOE_NO_MFMA) return kPlanGemv;
+    if (!(L.flags & WL_MOE_FORCE_MFMA) && T <= kGemvMaxTokens) return kPlanGemv;  // no expert can exceed 8 pairs
+    if (!prefill_eligible(L, T)) return kPlanGemv;
+    return (L.flags & WL_MOE_FORCE_MFMA) ? kPlanMfma : kPlanSplit;
 }
 
 }  // namespace wl
@@ -938,8 +1066,10 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
     auto mark = record;
     mark(0);
-    // on the MFMA path the router also writes x as bf16 and the sort also writes the GEMM tile lists
-    const bool mfma = prefill_eligible(L, tokens);
+    // an MFMA plan: the router also writes x as bf16 and the sort also writes the GEMM tile lists
+    const ExpertPlan plan = expert_plan(L, tokens);
+    const bool mfma = plan != kPlanGemv;
+    const int gemv_max = plan_gemv_max(plan);
     rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s)
                                          : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
     if (rc) return rc;
@@ -947,22 +1077,34 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
     if (rc) return rc;
     mark(2);
-    rc = launch_sort(L, w, w.ids, tokens, mfma, s);
+    rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, s);
     if (rc) return rc;
     mark(3);
-    if (mfma) {  // bf16 MFMA GEMMs (gate_up + SwiGLU in one stage, down in the next)
-        rc = launch_prefill_experts(L, x, tokens, w, s);
-        if (rc) return rc;
-        mark(4);
-    } else {
-        rc = launch_gemv_experts(L, x, tokens, w, s, mark);
+    // routed experts that may run on the GEMV kernels: each holds between 1 and gemv_max pairs
+    const int64_t P = tokens * L.top_k;
+    const int max_gemv = plan == kPlanMfma ? 0 : static_cast<int>(P < L.n_experts ? P : L.n_experts);
+    // the shared expert runs on the MFMA GEMMs in an MFMA plan (it sees every token), else on the GEMV kernels
+    const ExpertArgs ga = gemv_args(L, x, tokens, w, max_gemv, shared && !mfma);
+    if (mfma) {
+        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, s);
         if (rc) return rc;
     }
+    launch_gemv_gate_up(L, ga, max_gemv, shared && !mfma, s);
+    rc = launch_status();
+    if (rc) return rc;
+    mark(4);
+    if (mfma) {
+        rc = launch_mfma_down(L, tokens, w, gemv_max, s);
+        if (rc) return rc;
+    }
+    launch_gemv_down(L, ga, max_gemv, shared && !mfma, s);
+    rc = launch_status();
+    if (rc) return rc;
     mark(5);
     const unsigned cgrid = static_cast<unsigned>(tokens * ((L.hidden + kCombineSpan - 1) / kCombineSpan));
     if (mfma)
         k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                                  w.wts, reinterpret_cast<const uint16_t*>(w.o),
+                                                  w.wts, w.o,
                                                   shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg, y);
     else
         k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
@@ -992,7 +1134,7 @@ int wl_moe_stage_count(void) { return kMoeStages; }
 int wl_moe_plan(const WlMoeLayer* layer, int64_t tokens) {
     if (check_layer(layer) != WL_OK || tokens <= 0) return -1;
     if (fused_eligible(*layer, tokens)) return 1;
-    return prefill_eligible(*layer, tokens) ? 2 : 0;
+    return static_cast<int>(expert_plan(*layer, tokens));
 }
 
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {

@@ -491,6 +491,19 @@ __device__ __forceinline__ float silu_bf16(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
 }
 
+// Two bf16 values of the SwiGLU product from fp32 gate and up sums, rounded where the reference's bf16 tensors
+// round them (engines/base.py:568-570 on bf16 F.linear outputs): the gate_up matmul returns gate and up as bf16,
+// F.silu(gate) returns bf16, and so does silu(gate) * up (the product of two bf16 values is exact in fp32, so
+// only its final rounding matters). Returns the packed pair (value 0 in the low half).
+__device__ __forceinline__ uint32_t swiglu_bf16(float g0, float u0, float g1, float u1) {
+    const uint32_t gp = pack2(g0, g1), up = pack2(u0, u1);
+    const float gb0 = __builtin_bit_cast(float, gp << 16), gb1 = __builtin_bit_cast(float, gp & 0xFFFF0000u);
+    const float ub0 = __builtin_bit_cast(float, up << 16), ub1 = __builtin_bit_cast(float, up & 0xFFFF0000u);
+    const uint32_t sp = pack2(silu_bf16(gb0), silu_bf16(gb1));
+    const float sb0 = __builtin_bit_cast(float, sp << 16), sb1 = __builtin_bit_cast(float, sp & 0xFFFF0000u);
+    return pack2(sb0 * ub0, sb1 * ub1);
+}
+
 // A wavefront-uniform pointer in scalar registers (the value of lane 0).
 __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
@@ -728,9 +741,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
                 if (t < count) {
                     const int j = j0 + 16 * r + 4 * q;
                     const floatx4 g = acc[r][n], u = acc[r + kHalf][n];
-                    const uint2 v = make_uint2(pack2(silu_bf16(g[0]) * u[0], silu_bf16(g[1]) * u[1]),
-                                               pack2(silu_bf16(g[2]) * u[2], silu_bf16(g[3]) * u[3]));
-                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j) = v;
+                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j) =
+                        make_uint2(swiglu_bf16(g[0], u[0], g[1], u[1]), swiglu_bf16(g[2], u[2], g[3], u[3]));
                 }
             }
         }
@@ -739,9 +751,10 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
 }
 
 // down: a workgroup takes a.down_slabs consecutive 256-row slabs of the hidden dim (one pipeline across them); for
-// slab item, wavefront w has rows 256 (slab0 + item) + 16 kRT w + 16 r + lr. o by position, rounded to bf16 as the
-// reference's bf16 F.linear output is (gguf/metal.py:407). Its tiles hold at
-// most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts within 256 registers).
+// slab item, wavefront w has rows 256 (slab0 + item) + 16 kRT w + 16 r + lr. o by position (row stride a.ldo;
+// the shared expert's by token, stride H), rounded to bf16 as the reference's bf16 F.linear output is
+// (gguf/metal.py:407). Its tiles hold at most 128 tokens (8 token tiles of accumulators keep Q6_K's wavefronts
+// within 256 registers).
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kDownTileTokens>()];
@@ -769,6 +782,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     };
     auto src_row = [&](int t) -> int64_t { return pos0 + t; };
     uint16_t* out = sh ? a.o_sh16 : a.o16;
+    const int64_t ldo = sh ? a.H : a.ldo;
     auto epi = [&](int item, floatx4 (&acc)[kRT][kDownTileTokens / 16]) {
         const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -778,7 +792,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
                 const int t = 16 * n + lr;
                 if (t < count) {
                     const floatx4 v = acc[r][n];
-                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * a.H + row0 + 256 * item +
+                    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * ldo + row0 + 256 * item +
                                               16 * r + 4 * q) = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
                 }
             }
@@ -806,9 +820,12 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
     return launch_status();
 }
 
-int max_tiles(const WlMoeLayer& L, int64_t T, int cap) {
+// The most GEMM tiles a call can need: an MFMA expert holds c > gemv_max pairs and ceil(c / cap) tiles, at most
+// c / cap + 1, so the routed tiles number at most P / cap + (experts that can hold more than gemv_max pairs).
+int max_tiles(const WlMoeLayer& L, int64_t T, int cap, int gemv_max) {
     const int64_t P = T * L.top_k;
-    const int64_t routed = (P + cap - 1) / cap + L.n_experts;
+    const int64_t big = P / (static_cast<int64_t>(gemv_max) + 1);
+    const int64_t routed = (P + cap - 1) / cap + (big < L.n_experts ? big : L.n_experts);
     const int64_t shared = L.shared_gate_up ? (T + cap - 1) / cap : 0;
     return static_cast<int>(routed + shared);
 }
@@ -822,14 +839,14 @@ constexpr int64_t kDownMinGroups = 1024;
 constexpr int64_t kDownFewTokens = 256;
 static int down_slabs(const WlMoeLayer& L, int64_t T) {
     const int nslab = L.hidden / 256;
-    const int64_t tiles = max_tiles(L, T, kDownTileTokens) - L.n_experts;  // about the full tiles
+    const int64_t tiles = (T * L.top_k + kDownTileTokens - 1) / kDownTileTokens;  // about the full tiles
     if (T <= kDownFewTokens && nslab % 2 == 0) return 2;
     int p = 1;
     while (p < kDownSlabsMax && nslab % (2 * p) == 0 && tiles * nslab / (2 * p) >= kDownMinGroups) p *= 2;
     return p;
 }
 
-int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, hipStream_t s) {
+static PrefillArgs prefill_args(const WlMoeLayer& L, int64_t T, const Workspace& w) {
     const bool shared = L.shared_gate_up != nullptr;
     PrefillArgs a{};
     a.gate_up = static_cast<const uint8_t*>(L.gate_up);
@@ -846,26 +863,45 @@ int launch_prefill_experts(const WlMoeLayer& L, const float* x, int64_t T, const
     a.n_tiles_down = w.n_tiles + 1;
     a.h16 = w.h16;
     a.h_sh16 = w.h_sh16;
-    a.o16 = reinterpret_cast<uint16_t*>(w.o);  // the fp32 buffers, half used
+    // the routed outputs share the fp32 buffer with the GEMV experts' outputs: position pos's bf16 row fills the
+    // first half of its fp32 row (stride 2 H values)
+    a.o16 = reinterpret_cast<uint16_t*>(w.o);
+    a.ldo = 2 * static_cast<int64_t>(L.hidden);
     a.o_sh16 = reinterpret_cast<uint16_t*>(w.o_sh);
     a.H = L.hidden;
     a.inter = L.inter;
     a.sh_inter = shared ? L.shared_inter : 0;
     a.E = L.n_experts;
     a.k = L.top_k;
-    const int tiles8 = (max_tiles(L, T, kTileTokens) + kXcds - 1) / kXcds * kXcds;
-    const int tiles8_down = (max_tiles(L, T, kDownTileTokens) + kXcds - 1) / kXcds * kXcds;
     const int inter_max = shared && L.shared_inter > L.inter ? L.shared_inter : L.inter;
     a.nslab_gate_up = (inter_max + 127) / 128;
-    // the routed and shared experts share one launch, so their types must agree (checked by prefill_eligible)
+    a.down_slabs = down_slabs(L, T);
+    return a;
+}
+
+static int tiles8(const WlMoeLayer& L, int64_t T, int cap, int gemv_max) {
+    return (max_tiles(L, T, cap, gemv_max) + kXcds - 1) / kXcds * kXcds;
+}
+
+// The MFMA experts' gate_up + SwiGLU (the routed experts with more than gemv_max pairs and the shared expert).
+// The routed and shared experts share one launch, so their types must agree (checked by prefill_eligible).
+int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s) {
+    const PrefillArgs a = prefill_args(L, T, w);
     if (L.gate_up_type == WL_TYPE_Q4_K)
         k_gemm_gate_up<WL_TYPE_Q4_K, kTileTokens>
-            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8)), kGemmThreads, 0, s>>>(a);
+            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max))), kGemmThreads, 0,
+               s>>>(a);
     else
         k_gemm_gate_up<WL_TYPE_Q6_K, kDownTileTokens>
-            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8_down)), kGemmThreads, 0, s>>>(a);
-    a.down_slabs = down_slabs(L, T);
-    const dim3 g2(static_cast<unsigned>(L.hidden / 256 / a.down_slabs * tiles8_down));
+            <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kDownTileTokens, gemv_max))), kGemmThreads,
+               0, s>>>(a);
+    return launch_status();
+}
+
+// The MFMA experts' down products.
+int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s) {
+    const PrefillArgs a = prefill_args(L, T, w);
+    const dim3 g2(static_cast<unsigned>(L.hidden / 256 / a.down_slabs * tiles8(L, T, kDownTileTokens, gemv_max)));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
     else
@@ -882,6 +918,7 @@ int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x
     a.down_stride = 0;
     a.h16 = const_cast<uint16_t*>(x);
     a.o16 = y;
+    a.ldo = rows;
     a.H = rows;
     a.inter = k;
     a.E = 1;  // the one matrix is expert 0, never the shared slot
@@ -896,11 +933,8 @@ int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x
     return launch_status();
 }
 
+// Whether the layer's shapes and types let the MFMA GEMMs run (expert_plan decides when they do).
 bool prefill_eligible(const WlMoeLayer& L, int64_t T) {
-    if (L.flags & WL_MOE_NO_MFMA) return false;
-    // the reference's own split (gguf/metal.py:20,401-408): up to MAX_TOKENS tokens its exact-weight GEMV, above
-    // that a bf16 matmul of the weights dequantized to bf16
-    if (!(L.flags & WL_MOE_FORCE_MFMA) && T <= kGemvMaxTokens) return false;
     if (L.hidden % 256 != 0 || L.inter % 128 != 0) return false;
     if (L.shared_gate_up && (L.shared_gate_up_type != L.gate_up_type || L.shared_down_type != L.down_type ||
                              L.shared_inter % 128 != 0))

@@ -86,10 +86,14 @@ class MoELayer:
         return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
 
     def plan(self, tokens: int) -> str:
-        """'fused' (one persistent kernel, 1 token), 'gemv' (fp32 expert kernels, up to 8 tokens) or 'mfma' (bf16
-        MFMA expert GEMMs, more than 8: the reference's own split, gguf/metal.py:20,401-408) for this many tokens;
-        mfma='never' / 'always' at construction pins the choice."""
-        return {1: "fused", 2: "mfma", 0: "gemv"}[library().wl_moe_plan(ctypes.byref(self.struct), tokens)]
+        """How a call with this many tokens runs: 'fused' (one persistent kernel, 1 token); 'gemv' (every expert on
+        the fp32 GEMV kernels); 'split' (each expert by its own token count, as the reference's each_expert hands
+        F.linear only that expert's tokens, engines/base.py:566-571, and GGMLWeight.linear switches at
+        MAX_TOKENS = 8, gguf/metal.py:20,404-407: an expert with more than 8 tokens, and the shared expert, on the
+        bf16 MFMA GEMMs, the rest on GEMV); 'mfma' (every expert on the MFMA GEMMs). mfma='never' / 'always' at
+        construction pins 'gemv' / 'mfma'."""
+        return {1: "fused", 0: "gemv", 2: "split", 3: "mfma"}[library().wl_moe_plan(ctypes.byref(self.struct),
+                                                                                    tokens)]
 
     def workspace(self, tokens: int) -> torch.Tensor:
         need = self.workspace_bytes(tokens)
@@ -97,14 +101,30 @@ class MoELayer:
             self._ws = new_workspace(need, self.device)
         return self._ws
 
+    def _check_out(self, t, name, dtype, shape):
+        if t is None:
+            return
+        if t.dtype != dtype or tuple(t.shape) != shape or not t.is_contiguous() or t.device != self.device:
+            raise ValueError(f"{name} must be a contiguous {dtype} tensor of shape {list(shape)} on {self.device} "
+                             f"(got {t.dtype} {list(t.shape)} on {t.device}"
+                             f"{'' if t.is_contiguous() else ', not contiguous'})")
+
     def __call__(self, x: torch.Tensor, out: torch.Tensor = None, ids: torch.Tensor = None,
                  weights: torch.Tensor = None, workspace: torch.Tensor = None) -> torch.Tensor:
         """x [T, hidden] -> fp32 [T, hidden] (written into `out` when given). ids int32 / weights fp32 [T, top_k]
-        receive the routing when given."""
+        receive the routing when given. Every given output must be contiguous, of its dtype and shape, on the
+        layer's device; a workspace must be a uint8 device tensor of at least workspace_bytes(T) bytes prepared
+        by new_workspace."""
         _on_gpu(x, "x")
-        xf = x.reshape(-1, self.hidden).to(torch.float32).contiguous()
+        xf = x.reshape(-1, self.hidden).to(device=self.device, dtype=torch.float32).contiguous()
         tokens = xf.shape[0]
+        self._check_out(out, "out", torch.float32, (tokens, self.hidden))
+        self._check_out(ids, "ids", torch.int32, (tokens, self.top_k))
+        self._check_out(weights, "weights", torch.float32, (tokens, self.top_k))
         y = out if out is not None else torch.empty(tokens, self.hidden, dtype=torch.float32, device=self.device)
+        if workspace is not None and (workspace.dtype != torch.uint8 or workspace.device != self.device
+                                      or not workspace.is_contiguous()):
+            raise ValueError("workspace must be a contiguous uint8 tensor on the layer's device")
         ws = workspace if workspace is not None else self.workspace(tokens)
         check(library().wl_moe_layer(ctypes.byref(self.struct), xf.data_ptr(), tokens, y.data_ptr(), _ptr(ids),
                                      _ptr(weights), ws.data_ptr(), ws.numel(), _stream(self.device)))
