@@ -42,6 +42,7 @@ extern "C" {
 #define WL_EINVAL_WORKSPACE -6 /* workspace NULL or smaller than wl_moe_workspace_bytes() */
 #define WL_EINVAL_DTYPE -7     /* output dtype is not WL_DTYPE_F32 / WL_DTYPE_BF16 */
 #define WL_EINVAL_COUNT -8     /* too many experts for one batched call */
+#define WL_EINVAL_SCRATCH -9   /* wl_moe_layer_noalloc: the call needs more than WL_NOALLOC_SCRATCH_BYTES */
 
 #define WL_MAX_TOPK 16
 #define WL_MAX_BATCH_EXPERTS 64 /* experts per wl_gemv_batch / wl_gemv_combine call */
@@ -164,6 +165,22 @@ int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens
 /* Number of stages wl_moe_layer runs, and their names ("router", "topk", "sort", "gate_up", "down", "combine"). */
 int wl_moe_stage_count(void);
 const char* wl_moe_stage_name(int stage);
+
+/* Bytes of the device scratch array wl_moe_layer_noalloc runs on (one copy per GPU, held until the process ends).
+ * It covers calls whose wl_moe_workspace_bytes() is up to this size: at Qwen3.6-35B-A3B's shapes (hidden 2048, 256 experts
+ * of width 512, top-8, shared expert) up to 128 tokens. */
+#define WL_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* wl_moe_layer without a workspace and without allocating anything: the workspace is a file-scope device array of
+ * WL_NOALLOC_SCRATCH_BYTES on the current device (its address is looked up, and its synchronization words zeroed
+ * by a fill kernel on `stream`, on the first call on each device). For callers that cannot allocate: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. Calls that need more than the scratch
+ * holds return WL_EINVAL_SCRATCH before enqueuing anything. Every call on a device shares that device's scratch, so
+ * calls that overlap on one GPU (different streams, or host threads) race: order them on one stream. The caller
+ * still passes x, y and (optionally) ids / weights, as for wl_moe_layer, with the same results.
+ * No counterpart in the reference (whose MoE layer allocates per call); it is for callers that cannot allocate. */
+int wl_moe_layer_noalloc(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
+                         float* weights, void* stream);
 
 #ifdef __cplusplus
 }

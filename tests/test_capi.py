@@ -32,7 +32,7 @@ def test_abi_version_and_struct_layout():
 
 def test_error_strings():
     lib = hip.library()
-    for code in range(-8, 1):
+    for code in range(-9, 1):
         assert lib.wl_error_string(code)
     assert b"unsupported" in lib.wl_error_string(-1)
 
@@ -131,3 +131,21 @@ def test_python_errors():
         hip.check(1)
     with pytest.raises(NotImplementedError):
         hip._type_id("IQ4_XS")
+
+
+def test_noalloc_validation_without_a_gpu():
+    """wl_moe_layer_noalloc checks the layer and the size it would need before touching the device."""
+    lib = hip.library()
+    s = hip.WlMoeLayer()
+    s.gate_up = s.down = s.router = s.shared_gate_up = s.shared_down = s.shared_gate = FAKE
+    s.gate_up_stride, s.down_stride = 1179648, 860160
+    s.gate_up_type = s.shared_gate_up_type = 12
+    s.down_type = s.shared_down_type = 14
+    s.hidden, s.inter, s.shared_inter, s.n_experts, s.top_k, s.norm_topk_prob = 2048, 512, 512, 256, 8, 1
+    assert lib.wl_moe_workspace_bytes(ctypes.byref(s), 128) <= hip.NOALLOC_SCRATCH_BYTES
+    assert lib.wl_moe_workspace_bytes(ctypes.byref(s), 4096) > hip.NOALLOC_SCRATCH_BYTES
+    assert lib.wl_moe_layer_noalloc(ctypes.byref(s), FAKE, 4096, FAKE, None, None, None) == -9
+    assert lib.wl_moe_layer_noalloc(ctypes.byref(s), FAKE, 0, FAKE, None, None, None) == -2
+    assert lib.wl_moe_layer_noalloc(ctypes.byref(s), None, 1, FAKE, None, None, None) == -3
+    s.top_k = 0
+    assert lib.wl_moe_layer_noalloc(ctypes.byref(s), FAKE, 1, FAKE, None, None, None) == -5

@@ -3,6 +3,8 @@
 // the Metal gemv_batch / gemv_combine launches it makes; routing never leaves the GPU (no host sync per layer).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "wl_common.h"
 #include "wl_host.h"
 #include "wl_moe.h"
@@ -1005,6 +1007,9 @@ const char* wl_error_string(int code) {
         case WL_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wl_moe_workspace_bytes()";
         case WL_EINVAL_DTYPE: return "output dtype must be WL_DTYPE_F32 or WL_DTYPE_BF16";
         case WL_EINVAL_COUNT: return "expert count must be in 1..64";
+        case WL_EINVAL_SCRATCH:
+            return "the call needs more workspace than wl_moe_layer_noalloc's scratch holds "
+                   "(WL_NOALLOC_SCRATCH_BYTES): use wl_moe_layer with a workspace";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -1150,3 +1155,67 @@ const char* wl_moe_stage_name(int stage) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------------------------------
+// The no-allocation entry point: wl_moe_layer on a workspace that is a file-scope device array. Each GPU the
+// library runs on holds its own copy of `scratch` (WL_NOALLOC_SCRATCH_BYTES) until the process ends. Host code never
+// uses the array's name as a device address: on a call's first use of a device, with that device current,
+// hipGetSymbolAddress gives this device's copy, which is kept per device and used for everything after, and the
+// fused kernel's synchronization words at its start are zeroed there (a fill kernel on the caller's stream; the
+// array is zero at load too). Calls keep those words consistent afterwards.
+namespace wl {
+
+static __device__ __attribute__((aligned(256))) uint8_t scratch[WL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];  // this device's copy of `scratch`, once set up
+static std::mutex g_scratch_lock;
+
+// The current device's scratch address, set up on first use (hipGetSymbolAddress, then the sync words zeroed on
+// `s`); nullptr with *rc set when that fails.
+static void* scratch_address(hipStream_t s, int* rc) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *rc = static_cast<int>(e);
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        *rc = WL_EINVAL_SHAPE;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *rc = e != hipSuccess ? static_cast<int>(e) : WL_EINVAL_NULL;
+            return nullptr;
+        }
+        const int z = zero_sync(ptr, s);
+        if (z != WL_OK) {
+            *rc = z;
+            return nullptr;
+        }
+        g_scratch[dev] = ptr;
+    }
+    *rc = WL_OK;
+    return g_scratch[dev];
+}
+
+}  // namespace wl
+
+extern "C" int wl_moe_layer_noalloc(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y,
+                                    int32_t* ids, float* weights, void* stream) {
+    using namespace wl;
+    const int rc0 = check_layer(layer);
+    if (rc0) return rc0;
+    if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
+    if (carve(*layer, tokens, nullptr).bytes > WL_NOALLOC_SCRATCH_BYTES) return WL_EINVAL_SCRATCH;
+    if (!x || !y) return WL_EINVAL_NULL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int rc = WL_OK;
+    void* ws = scratch_address(s, &rc);
+    if (!ws) return rc;
+    return run_layer(layer, x, tokens, y, ids, weights, ws, WL_NOALLOC_SCRATCH_BYTES, stream, nullptr);
+}

@@ -130,6 +130,21 @@ class MoELayer:
                                      _ptr(weights), ws.data_ptr(), ws.numel(), _stream(self.device)))
         return y
 
+    def call_noalloc(self, x: torch.Tensor, out: torch.Tensor, ids: torch.Tensor = None,
+                     weights: torch.Tensor = None) -> torch.Tensor:
+        """The layer through wl_moe_layer_noalloc: no workspace, nothing allocated by the library (its scratch is a
+        device array of NOALLOC_SCRATCH_BYTES per GPU, shared by every such call on that GPU). x must already be a
+        contiguous fp32 [T, hidden] device tensor and out is required, so this call allocates nothing either."""
+        if x.dtype != torch.float32 or not x.is_contiguous() or x.device != self.device or x.dim() != 2:
+            raise ValueError("x must be a contiguous fp32 [T, hidden] tensor on the layer's device")
+        tokens = x.shape[0]
+        self._check_out(out, "out", torch.float32, (tokens, self.hidden))
+        self._check_out(ids, "ids", torch.int32, (tokens, self.top_k))
+        self._check_out(weights, "weights", torch.float32, (tokens, self.top_k))
+        check(library().wl_moe_layer_noalloc(ctypes.byref(self.struct), x.data_ptr(), tokens, out.data_ptr(),
+                                             _ptr(ids), _ptr(weights), _stream(self.device)))
+        return out
+
     def route(self, x: torch.Tensor, return_logits: bool = False):
         """-> (weights fp32 [T, top_k], ids int32 [T, top_k], shared gate fp32 [T] or None): engines/base.py:91-97
         on the router logits, plus sigmoid(x . shared_gate); with return_logits also the logits fp32 [T, E]
