@@ -43,6 +43,7 @@ extern "C" {
 #define WL_EINVAL_DTYPE -7     /* output dtype is not WL_DTYPE_F32 / WL_DTYPE_BF16 */
 #define WL_EINVAL_COUNT -8     /* too many experts for one batched call */
 #define WL_EINVAL_SCRATCH -9   /* wl_moe_layer_noalloc: the call needs more than WL_NOALLOC_SCRATCH_BYTES */
+#define WL_ESYNC -10           /* wl_moe_workspace_status: a fused-kernel wait gave up since the last query */
 
 #define WL_MAX_TOPK 16
 #define WL_MAX_BATCH_EXPERTS 64 /* experts per wl_gemv_batch / wl_gemv_combine call */
@@ -110,12 +111,22 @@ typedef struct WlMoeLayer {
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */
 #define WL_MOE_NO_MFMA 2         /* flags: every expert on the fp32 GEMV kernels at any token count */
 #define WL_MOE_FORCE_MFMA 4      /* flags: every expert on the bf16 MFMA GEMMs at any token count (testing) */
+#define WL_MOE_TEST_STARVE 8     /* flags, testing only: in the fused kernel one workgroup withholds its results and
+                                    the others' bounded waits give up early, so the call ends with NaN outputs and
+                                    the workspace's status word set (the failure wl_moe_workspace_status reports) */
 
 /* Checks a layer description without touching device memory; 0 or a WL_E* code. */
 int wl_moe_check(const WlMoeLayer* layer);
 
 /* Bytes of device workspace wl_moe_layer needs for `tokens` tokens (0 on an invalid layer). */
 size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
+
+/* The fused kernel's health since the previous query on this workspace (NULL: the current device's
+ * wl_moe_layer_noalloc scratch). Its hand-offs between workgroups need the whole grid resident at once; the
+ * library checks that before it launches, and every wait is bounded, so a workgroup that still waits too long gives
+ * up, writes NaN for its outputs and sets a status word. This synchronizes `stream`, reads and clears the word, and
+ * returns WL_OK, WL_ESYNC when it was set, or a hipError_t. Not for use under stream capture. */
+int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Zeroes the synchronization words at the start of a workspace (the fused decode kernel's per-workgroup epoch
  * counters and epoch-tagged exchange slots) with a fill kernel on `stream`. Call once after allocating a workspace, before its first

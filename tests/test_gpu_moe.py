@@ -251,3 +251,26 @@ def test_prefill_mfma_variants(hip, variant):
     layer = hip.MoELayer.from_host(lw, mfma="always")
     T = 37 if variant == "partial_tiles" else 300  # 300 * 4 / 16 = 75 tokens per expert on average
     check_prefill(hip, layer, lw, synth.tokens(71, T, kw["hidden"]), variant)
+
+
+def test_fused_give_up_is_reported(hip, layer_c2):
+    """The fused kernel's hand-offs need every workgroup resident; a wait that runs out gives up rather than hang.
+    Forced from the host (WL_MOE_TEST_STARVE: one workgroup withholds its results, the other waits give up after
+    a short bounded spin, so every workgroup still exits): the outputs hold NaN, wl_moe_workspace_status reports
+    ESYNC once and clears it, and the next ordinary call on the same workspace is correct."""
+    layer = hip.MoELayer.from_host(layer_c2)
+    starved = hip.MoELayer.from_host(layer_c2)
+    starved.struct.flags |= hip.MOE_TEST_STARVE
+    assert layer.plan(1) == "fused" and starved.plan(1) == "fused"
+    ws = layer.workspace(1)
+    x = synth.tokens(40, 1)
+    xt = torch.from_numpy(x).cuda()
+    assert layer.status(ws) == 0
+    y_bad = starved(xt, workspace=ws).cpu().numpy()
+    assert np.isnan(y_bad).any()
+    assert layer.status(ws) == hip.ESYNC
+    assert layer.status(ws) == 0  # reported once, then cleared
+    y = layer(xt, workspace=ws).cpu().numpy()
+    assert layer.status(ws) == 0
+    assert np.isfinite(y).all()
+    assert moe_ref.rel_err(y, moe_ref.layer(x, layer_c2)) < TOL

@@ -29,7 +29,9 @@ constexpr int kFlagStride = 32;       // words between workgroups' epoch counter
 constexpr int kTagLogits = kFlagStride * kFusedMaxG;
 constexpr int kTagHsh = kTagLogits + 2 * (kFusedMaxE + 16);
 constexpr int kTagH = kTagHsh + 2 * kFusedMaxInter;
-constexpr int kSyncWords = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
+// then the status word: nonzero once a fused-kernel workgroup's bounded wait gave up (wl_moe_workspace_status)
+constexpr int kStatusWord = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
+constexpr int kSyncWords = kStatusWord + kFlagStride;
 
 struct ExpertArgs {
     const uint8_t* gate_up;
@@ -119,6 +121,7 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T);
 int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, float* wts, const Workspace& w,
                  hipStream_t s);
 int zero_sync(void* workspace, hipStream_t s);
+int zero_words(uint32_t* p, int n, hipStream_t s);  // a fill kernel (no hipMemsetAsync: graph-capture safe)
 // How the routed experts of a T-token call are run: kPlanGemv (every expert on the fp32 GEMV kernels), kPlanSplit
 // (experts with more than kGemvMaxTokens tokens on the MFMA GEMMs, the rest on GEMV), kPlanMfma (every expert on
 // the MFMA GEMMs; WL_MOE_FORCE_MFMA). The fused single-kernel decode is chosen before this (fused_eligible).

@@ -1007,6 +1007,9 @@ const char* wl_error_string(int code) {
         case WL_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wl_moe_workspace_bytes()";
         case WL_EINVAL_DTYPE: return "output dtype must be WL_DTYPE_F32 or WL_DTYPE_BF16";
         case WL_EINVAL_COUNT: return "expert count must be in 1..64";
+        case WL_ESYNC:
+            return "a fused-kernel workgroup gave up waiting for another (not every workgroup was resident): the "
+                   "outputs of the calls since the last status query hold NaN";
         case WL_EINVAL_SCRATCH:
             return "the call needs more workspace than wl_moe_layer_noalloc's scratch holds "
                    "(WL_NOALLOC_SCRATCH_BYTES): use wl_moe_layer with a workspace";
@@ -1204,6 +1207,31 @@ static void* scratch_address(hipStream_t s, int* rc) {
 }
 
 }  // namespace wl
+
+extern "C" int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, void* stream) {
+    using namespace wl;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void* ws = workspace;
+    if (!ws) {
+        int rc = WL_OK;
+        ws = scratch_address(s, &rc);
+        if (!ws) return rc;
+    } else {
+        if (workspace_bytes < sizeof(uint32_t) * kSyncWords) return WL_EINVAL_WORKSPACE;
+        if (reinterpret_cast<uintptr_t>(workspace) % 256) return WL_EINVAL_ALIGN;
+    }
+    uint32_t* word = static_cast<uint32_t*>(ws) + kStatusWord;
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return static_cast<int>(e);
+    uint32_t v = 0;
+    e = hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!v) return WL_OK;
+    int rc = zero_words(word, 1, s);
+    if (rc) return rc;
+    e = hipStreamSynchronize(s);
+    return e != hipSuccess ? static_cast<int>(e) : WL_ESYNC;
+}
 
 extern "C" int wl_moe_layer_noalloc(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y,
                                     int32_t* ids, float* weights, void* stream) {

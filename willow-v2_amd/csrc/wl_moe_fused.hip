@@ -29,13 +29,17 @@
 // this call's epoch, so a consumer polls the data itself until every word it needs carries the current tag.
 // Each workgroup keeps its own epoch counter (one 128-byte line each, incremented as it exits), so all agree on
 // the epoch without communicating and nothing is ever reset. Every wait is bounded (kSpinLimit polls): a
-// workgroup that gives up writes NaN instead of hanging.
+// workgroup that gives up writes NaN for its outputs and sets the workspace's status word, which
+// wl_moe_workspace_status reports (and clears) on the host. Co-residency of the whole grid is what the hand-offs
+// need; launch_fused checks it for the exact kernel instance it launches.
 #include <hip/hip_runtime.h>
 
 #include "wl_common.h"
 #include "wl_host.h"
 #include "wl_moe.h"
 #include "wl_moe_dev.h"
+
+#include <mutex>
 
 namespace wl {
 
@@ -44,6 +48,7 @@ constexpr int kFusedWaves = kFusedThreads / 64;
 constexpr int kGateUpTasks = 2;  // gate_up tasks a wavefront has in flight at once (G = 256: all of them)
 constexpr int kOwnRows = 8;      // output rows per owner group: the shared and routed down rows and the final sum
 constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kStarveSpinLimit = 1u << 11;  // WL_MOE_TEST_STARVE: waits known to fail give up after this
 static_assert(kFusedThreads >= kFusedMaxE && kFusedMaxE % 32 == 0 && kFusedMaxE / 32 >= kFusedMaxK,
               "the top-k gives every logit a thread and needs at least k groups of 32");
 
@@ -61,8 +66,10 @@ struct FusedArgs {
     float* y;
     int32_t* ids_out;
     float* wts_out;
-    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I]
+    uint32_t* sync;  // kSyncWords: epochs, then tagged logits [E+1], h_shared [I], h [k, I], the status word
     int H, I, E, k, renorm, G;
+    uint32_t spin_limit;  // polls before a wait gives up
+    int silent_wg;        // WL_MOE_TEST_STARVE: this workgroup publishes nothing (-1: none)
 };
 
 __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32_t tag, float v) {
@@ -74,7 +81,8 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
 // Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset) into *dst(i) once
 // every one carries `tag` (workgroup-cooperative); false if kSpinLimit polls pass first. n <= 32 * blockDim.x.
 template <typename Src, typename Dst>
-__device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, Src src, Dst dst) {
+__device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit, Src src,
+                                              Dst dst) {
     uint32_t pending = 0;
     for (int q = 0; q < 32 && static_cast<int>(threadIdx.x) + q * static_cast<int>(blockDim.x) < n; q++)
         pending |= 1u << q;
@@ -92,7 +100,7 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
             }
         }
         if (__syncthreads_and(pending == 0)) return true;
-        if (spins >= kSpinLimit) return false;
+        if (spins >= spin_limit) return false;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -103,10 +111,11 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
 // are, and the bulk polls no longer load the memory system while the producers finish (17.90 -> 17.60 us per
 // layer). All Q loads of a polling round are issued before any is checked.
 template <int Q, typename Src, typename Dst>
-__device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_t tag, Src src, Dst dst) {
+__device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_t tag, uint32_t spin_limit, Src src,
+                                                   Dst dst) {
     static_assert(Q <= 32, "");
     const int lane = threadIdx.x & 63;
-    for (uint32_t spins = 0; spins < kSpinLimit; spins++) {
+    for (uint32_t spins = 0; spins < spin_limit; spins++) {
         const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(lane + 64 * (Q - 1))),
                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__all(static_cast<uint32_t>(w >> 32) == tag)) break;
@@ -127,7 +136,7 @@ __device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_
                 pending &= ~(1u << q);
             }
         if (__all(pending == 0)) return true;
-        if (spins >= kSpinLimit) return false;
+        if (spins >= spin_limit) return false;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -163,6 +172,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // every thread reads the epoch itself: no barrier, and the load overlaps the first weight loads
     const uint32_t tag = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     bool ok = true;
+    const bool publish = b != a.silent_wg;
 
     // x, for the gate_up dot products: a lane's two 16-value runs of its block gi
     const int nb = H / kQK;  // <= 8: one gate/up block per lane group
@@ -200,7 +210,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const bool valid = lane < 32;
             const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
             const float total = router_row(a.x, wr, valid, H, lane);
-            if ((lane & 31) == 0 && valid)
+            if ((lane & 31) == 0 && valid && publish)
                 put_tagged(a.sync, kTagLogits + 2 * row, tag,
                            (row < E && a.router_bias) ? __fadd_rn(total, a.router_bias[row]) : total);
         } else {
@@ -212,7 +222,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
             float g, u;
             gate_up_dots(lg, lu, g, u);
-            if (lane == 0) put_tagged(a.sync, kTagHsh + 2 * j, tag, silu(g) * u);
+            if (lane == 0 && publish) put_tagged(a.sync, kTagHsh + 2 * j, tag, silu(g) * u);
         }
     }
 
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading.
     __syncthreads();
     ok = gather_tagged(
-             a.sync, n_logits + (shared ? I : 0), tag,
+             a.sync, n_logits + (shared ? I : 0), tag, a.spin_limit,
              [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
              [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
          ok;
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
             float g, up;
             gate_up_dots(lg, lu, g, up);
-            if (lane == 0) put_tagged(a.sync, kTagH + 2 * u, tag, silu(g) * up);  // u = s * I + j
+            if (lane == 0 && publish) put_tagged(a.sync, kTagH + 2 * u, tag, silu(g) * up);  // u = s * I + j
         }
     }
 
@@ -409,7 +419,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             draw[p].fetch(w + static_cast<int64_t>(own_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
         float* hs = lds_h[wv];
         ok = gather_tagged_wave<4 * NBD>(
-                 a.sync, tag, [&](int i) { return kTagH + 2 * (wv * I + i); }, [&](int i) { return &hs[i]; }) &&
+                 a.sync, tag, a.spin_limit, [&](int i) { return kTagH + 2 * (wv * I + i); },
+                 [&](int i) { return &hs[i]; }) &&
              ok;
         lane_sync();
         float4 hl[4], hh[4];  // the lane's two runs of h: the same in every pass
@@ -435,6 +446,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if (shared) acc = acc + sgv * lds_sh[r];
         a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
     }
+    if (!all_ok && threadIdx.x == 0)  // a vector atomic, visible to the host's status query
+        __hip_atomic_fetch_or(a.sync + kStatusWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -445,45 +458,57 @@ __global__ void k_zero_words(uint32_t* p, int n) {
 
 // ---------------------------------------------------------------------------------------------------------------
 
-template <int GU, int DN, int EJ, int NBD>
-static hipError_t launch_fused_t(const FusedArgs& a, hipStream_t s) {
-    k_moe_decode<GU, DN, EJ, NBD><<<a.G, kFusedThreads, 0, s>>>(a);
-    return hipGetLastError();
-}
-
-template <int GU, int DN, int EJ>
-static hipError_t launch_fused_nbd(const FusedArgs& a, hipStream_t s) {
-    switch (a.I / kQK) {
-        case 1: return launch_fused_t<GU, DN, EJ, 1>(a, s);
-        case 2: return launch_fused_t<GU, DN, EJ, 2>(a, s);
-        default: return launch_fused_t<GU, DN, EJ, 4>(a, s);
+// The fused kernel instance a layer runs: gate_up Q4_K; down Q4_K or Q6_K; EJ logits per lane of the top-k; NBD
+// down blocks per row (inter / 256).
+static const void* fused_instance(const WlMoeLayer& L) {
+    const int ej = L.n_experts <= 64 ? 1 : L.n_experts <= 128 ? 2 : 4;
+    const int nbd = L.inter / kQK;
+#define WL_FUSED_PICK(DN)                                                                                          \
+    switch (ej * 8 + (nbd == 1 ? 1 : nbd == 2 ? 2 : 4)) {                                                           \
+        case 9: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 1>);                       \
+        case 10: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 2>);                      \
+        case 12: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 4>);                      \
+        case 17: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 1>);                      \
+        case 18: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 2>);                      \
+        case 20: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 4>);                      \
+        case 33: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 1>);                      \
+        case 34: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 2>);                      \
+        default: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 4>);                     \
     }
+    if (L.down_type == WL_TYPE_Q4_K) {
+        WL_FUSED_PICK(WL_TYPE_Q4_K)
+    }
+    WL_FUSED_PICK(WL_TYPE_Q6_K)
+#undef WL_FUSED_PICK
 }
 
-template <int GU, int DN>
-static hipError_t launch_fused_ej(const FusedArgs& a, hipStream_t s) {
-    if (a.E <= 64) return launch_fused_nbd<GU, DN, 1>(a, s);
-    if (a.E <= 128) return launch_fused_nbd<GU, DN, 2>(a, s);
-    return launch_fused_nbd<GU, DN, 4>(a, s);
-}
-
-// Workgroups of the persistent grid: one per CU of the current device (cached per device); 0 when the kernel
-// cannot keep one workgroup per CU resident.
-static int fused_grid() {
-    static int cached[64] = {0};
+// Workgroups of the persistent grid for `kernel`: one per CU of the current device, or 0 when this kernel instance
+// cannot keep one workgroup per CU resident (its hand-offs need the whole grid resident at once). Cached per device
+// and instance.
+static int fused_grid(const void* kernel) {
+    constexpr int kSlots = 32;
+    struct Entry {
+        const void* kernel;
+        int grid;
+    };
+    static Entry cache[64][kSlots] = {};
+    static std::mutex lock;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (!cached[dev]) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, WL_TYPE_Q6_K, 4, 2>),
-                kFusedThreads, 0) != hipSuccess || per_cu < 1)
-            return 0;
-        cached[dev] = cus < kFusedMaxG ? cus : kFusedMaxG;
+    std::lock_guard<std::mutex> guard(lock);
+    for (int i = 0; i < kSlots; i++) {
+        if (cache[dev][i].kernel == kernel) return cache[dev][i].grid;
+        if (!cache[dev][i].kernel) {
+            int cus = 0, per_cu = 0;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kFusedThreads, 0) != hipSuccess)
+                return 0;
+            const int grid = per_cu >= 1 ? (cus < kFusedMaxG ? cus : kFusedMaxG) : 0;
+            cache[dev][i] = Entry{kernel, grid};
+            return grid;
+        }
     }
-    return cached[dev];
+    return 0;
 }
 
 bool fused_eligible(const WlMoeLayer& L, int64_t T) {
@@ -496,7 +521,7 @@ bool fused_eligible(const WlMoeLayer& L, int64_t T) {
         return false;
     if (L.hidden % kOwnRows != 0 || L.hidden > kFusedMaxHidden) return false;
     // one pass per workgroup: an owner group at most, kGateUpTasks per wavefront at most
-    const int G = fused_grid();
+    const int G = fused_grid(fused_instance(L));
     const int64_t tasks = static_cast<int64_t>(L.top_k) * L.inter;
     return G >= 1 && L.hidden / kOwnRows <= G && tasks <= static_cast<int64_t>(kGateUpTasks) * kFusedWaves * G;
 }
@@ -523,14 +548,21 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
     a.E = L.n_experts;
     a.k = L.top_k;
     a.renorm = L.norm_topk_prob ? 1 : 0;
-    a.G = fused_grid();
-    hipError_t e = L.down_type == WL_TYPE_Q4_K ? launch_fused_ej<WL_TYPE_Q4_K, WL_TYPE_Q4_K>(a, s)
-                                               : launch_fused_ej<WL_TYPE_Q4_K, WL_TYPE_Q6_K>(a, s);
+    const void* kernel = fused_instance(L);
+    a.G = fused_grid(kernel);
+    if (a.G < 1) return WL_EINVAL_SHAPE;  // fused_eligible said otherwise: the device changed in between
+    const bool starve = (L.flags & WL_MOE_TEST_STARVE) != 0;
+    a.spin_limit = starve ? kStarveSpinLimit : kSpinLimit;
+    a.silent_wg = starve ? a.G - 1 : -1;
+    void* args[] = {&a};
+    const hipError_t e = hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a.G)), dim3(kFusedThreads), args, 0, s);
     return e == hipSuccess ? WL_OK : static_cast<int>(e);
 }
 
-int zero_sync(void* workspace, hipStream_t s) {
-    k_zero_words<<<32, 256, 0, s>>>(static_cast<uint32_t*>(workspace), kSyncWords);
+int zero_sync(void* workspace, hipStream_t s) { return zero_words(static_cast<uint32_t*>(workspace), kSyncWords, s); }
+
+int zero_words(uint32_t* p, int n, hipStream_t s) {
+    k_zero_words<<<(n + 255) / 256 < 32 ? (n + 255) / 256 : 32, 256, 0, s>>>(p, n);
     return launch_status();
 }
 

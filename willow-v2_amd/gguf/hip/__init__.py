@@ -20,7 +20,8 @@ BLOCK_SIZES = {"Q4_K": (256, 144), "Q6_K": (256, 210)}  # gguf/reader.py:25,27
 MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many tokens (gguf/metal.py:20)
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
-MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA = 1, 2, 4
+MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA, MOE_TEST_STARVE = 1, 2, 4, 8
+ESYNC = -10  # wl_moe_workspace_status: a fused-kernel wait gave up
 NOALLOC_SCRATCH_BYTES = 16 << 20  # WL_NOALLOC_SCRATCH_BYTES
 
 LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwillow_hip.so")
@@ -81,6 +82,7 @@ def library() -> ctypes.CDLL:
     lib.wl_moe_workspace_init.argtypes, lib.wl_moe_workspace_init.restype = [vp, ctypes.c_size_t, vp], c_int
     lib.wl_moe_stage_name.argtypes, lib.wl_moe_stage_name.restype = [c_int], ctypes.c_char_p
     lib.wl_moe_layer_noalloc.argtypes, lib.wl_moe_layer_noalloc.restype = [layer_p, vp, i64, vp, vp, vp, vp], c_int
+    lib.wl_moe_workspace_status.argtypes, lib.wl_moe_workspace_status.restype = [vp, ctypes.c_size_t, vp], c_int
     for name in ("wl_dequant", "wl_gemv", "wl_linear", "wl_gemv_batch", "wl_gemv_combine", "wl_moe_check", "wl_moe_route",
                  "wl_moe_layer", "wl_moe_layer_profile"):
         getattr(lib, name).restype = c_int
@@ -96,6 +98,8 @@ def check(rc: int):
     message = library().wl_error_string(rc).decode()
     if rc == -1:
         raise NotImplementedError(f"libwillow_hip: {message}")
+    if rc == ESYNC:
+        raise HipError(rc, message)
     if rc < 0:
         raise ValueError(f"libwillow_hip: {message} (code {rc})")
     raise HipError(rc, message)

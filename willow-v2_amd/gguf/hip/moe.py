@@ -145,6 +145,19 @@ class MoELayer:
                                              _ptr(ids), _ptr(weights), _stream(self.device)))
         return out
 
+    def status(self, workspace: torch.Tensor = None) -> int:
+        """wl_moe_workspace_status on `workspace` (default: this layer's own). Synchronizes the stream; returns 0,
+        or -10 (ESYNC) when a fused-kernel wait gave up since the previous query (the outputs of those calls hold
+        NaN)."""
+        ws = workspace if workspace is not None else self._ws
+        if ws is None:
+            return 0
+        return int(library().wl_moe_workspace_status(ws.data_ptr(), ws.numel(), _stream(self.device)))
+
+    def status_noalloc(self) -> int:
+        """wl_moe_workspace_status on the no-allocation entry point's scratch of this device."""
+        return int(library().wl_moe_workspace_status(None, 0, _stream(self.device)))
+
     def route(self, x: torch.Tensor, return_logits: bool = False):
         """-> (weights fp32 [T, top_k], ids int32 [T, top_k], shared gate fp32 [T] or None): engines/base.py:91-97
         on the router logits, plus sigmoid(x . shared_gate); with return_logits also the logits fp32 [T, E]
