@@ -451,121 +451,281 @@ __device__ __forceinline__ ExpertView expert_view(const ExpertArgs& a, int slot,
     return v;
 }
 
-// Both GEMV expert kernels handle an expert's tokens kGemvTok at a time: the workgroup first copies those tokens'
-// activation rows (x for gate_up, h for down) into LDS, all loads in flight at once, so their latency is paid once
-// per chunk, not once per token. In LDS a row of `width` values is padded by 4 floats after every 64 (lds_index),
-// which spreads the lanes' 16-byte reads over the banks. Then each wavefront decodes the weight blocks of several
-// rows once and runs every token of the chunk through them, reading the activations from LDS.
-constexpr int kGemvTok = 8;        // tokens per LDS chunk (an expert on the GEMV kernels has at most 8 in a split plan)
-constexpr int kGuRows = 4;         // gate_up: intermediate rows (a gate row and its up row) per wavefront
-constexpr int kDnPasses = 4;       // down: row passes per wavefront (R rows each)
-constexpr int kGemvLdsMax = 80 << 10;
+// The GEMV expert kernels run the few tokens of an expert (at most 8 when it shares a call with MFMA experts)
+// against exact fp32 weights. Layout: each 256-value block of a weight row belongs to one lane, and a row to L
+// consecutive lanes (L = the power of two <= min(blocks per row, 8); lane c takes blocks c, c + L, ...). A lane
+// loads its whole block at once, converts each of its values to fp32 once, and runs every token of the current
+// chunk through it: value = a q + b per sub-block (Q4_K: 32 values; Q6_K: 16), so a token adds
+// a * sum(q x) + b * sum(x) per sub-block, with sum(x) read from LDS. The chunk's activation rows (x for gate_up,
+// h for down) sit in LDS, staged once per chunk by the whole workgroup with all loads in flight at once: block kb of
+// a row starts at float 260 kb (4 floats of skew, so the 8 lanes reading 8 different blocks hit different banks;
+// the rows' other lanes read the same addresses, a broadcast), and the sums of every 16 values follow the rows.
+constexpr int kGemvTok = 8;         // most tokens per LDS chunk
+constexpr int kBlkFloats = 260;     // LDS floats per 256-value block of an activation row
+constexpr int kGemvLdsMax = 40 << 10;
 
-__host__ __device__ inline int lds_row_floats(int width) { return width + 4 * (width / 64); }
-__device__ __forceinline__ int lds_index(int i) { return i + 4 * (i >> 6); }
+__host__ __device__ inline int lds_row_floats(int width) { return width / 256 * kBlkFloats; }
+__host__ __device__ inline int lds_chunk_floats(int width) { return lds_row_floats(width) + width / 16; }
+
+// Tokens per chunk for activation rows of `width` values: at most kGemvTok, within kGemvLdsMax of LDS.
+__host__ inline int gemv_chunk(int width) {
+    const int per = kGemvLdsMax / (4 * lds_chunk_floats(width));
+    return per < 1 ? 1 : (per < kGemvTok ? per : kGemvTok);
+}
+
+// Lanes per row: the largest power of two <= min(blocks per row, 8).
+__host__ inline int gemv_lanes(int nb) { return nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1; }
+
+// rows u < n of the chunk: src_row(u)[0, width) -> LDS (rows of lds_row_floats(width), then the n rows' 16-value
+// sums, width / 16 each). Ends with a barrier.
+template <typename SrcRow>
+__device__ __forceinline__ void stage_chunk(float* lds, int n, int width, SrcRow src_row) {
+    const int per_row = width / 4, ld = lds_row_floats(width), ng = width / 16;
+    for (int f = threadIdx.x; f < n * per_row; f += blockDim.x) {
+        const int u = f / per_row, i = 4 * (f - u * per_row);
+        *reinterpret_cast<float4*>(lds + u * ld + (i >> 8) * kBlkFloats + (i & 255)) =
+            *reinterpret_cast<const float4*>(src_row(u) + i);
+    }
+    __syncthreads();
+    float* sums = lds + n * ld;
+    for (int f = threadIdx.x; f < n * ng; f += blockDim.x) {
+        const int u = f / ng, gg = f - u * ng;
+        float4 x[4];
+        const float4* q = reinterpret_cast<const float4*>(lds + u * ld + (gg >> 4) * kBlkFloats + 16 * (gg & 15));
+#pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = q[j];
+        sums[f] = sum16(x);
+    }
+    __syncthreads();
+}
+
+// sum of f[i] * x[i] for 16 values, x 16-byte aligned in LDS
+__device__ __forceinline__ float dot16_lds(const float* f, const float* x) {
+    const float4* q = reinterpret_cast<const float4*>(x);
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = q[i];
+        s0 = __builtin_fmaf(f[4 * i], v.x, s0);
+        s1 = __builtin_fmaf(f[4 * i + 1], v.y, s1);
+        s0 = __builtin_fmaf(f[4 * i + 2], v.z, s0);
+        s1 = __builtin_fmaf(f[4 * i + 3], v.w, s1);
+    }
+    return s0 + s1;
+}
+
+// the four bytes of w (fields of at most 8 bits) as floats into f[0..3]
+__device__ __forceinline__ void bytes_to_f32(uint32_t w, float* f) {
+    f[0] = ubyte(w, 0);
+    f[1] = ubyte(w, 1);
+    f[2] = ubyte(w, 2);
+    f[3] = ubyte(w, 3);
+}
+
+// acc[u] += (block . x_u) for the chunk's tokens u < n: xs = the block's 256 values of token 0 in LDS (token u at
+// xs + u ldx), ss = its 16 sums of token 0 (token u at ss + u lds_).
+template <int TYPE>
+struct BlockDot;
+
+template <>
+struct BlockDot<WL_TYPE_Q4_K> {
+    // blk: 16-byte aligned. Sub-block j = 2 q + e: values 64 q + 32 e + i are the low (e = 0) or high (e = 1)
+    // nibbles of qs bytes 32 q + i; value = (d sc_j) q - dmin m_j. fetch() issues the block's loads; run() uses
+    // them, so whatever runs in between (the activation staging) overlaps the loads.
+    uint4 hd, qv[8];
+    __device__ void fetch(const uint8_t* __restrict__ blk) {
+        const uint4* p = reinterpret_cast<const uint4*>(blk);
+        hd = p[0];
+#pragma unroll
+        for (int i = 0; i < 8; i++) qv[i] = p[1 + i];
+    }
+    __device__ void run(const float* xs, int ldx, const float* ss, int lds_, int n, float (&acc)[kGemvTok]) const {
+        const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t w[8] = {qv[2 * q].x, qv[2 * q].y, qv[2 * q].z, qv[2 * q].w,
+                                   qv[2 * q + 1].x, qv[2 * q + 1].y, qv[2 * q + 1].z, qv[2 * q + 1].w};
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int j = 2 * q + e;
+                uint32_t sc, m;
+                q4k_scale_min(j, hd.y, hd.z, hd.w, sc, m);
+                const float a = d * static_cast<float>(sc), b = -(dmin * static_cast<float>(m));
+                float f[32];
+#pragma unroll
+                for (int i = 0; i < 8; i++) bytes_to_f32(opaque((w[i] >> (4 * e)) & 0x0F0F0F0Fu), f + 4 * i);
+#pragma unroll
+                for (int u = 0; u < kGemvTok; u++) {
+                    if (u < n) {
+                        const float* x = xs + u * ldx + 32 * j;
+                        const float sq = dot16_lds(f, x) + dot16_lds(f + 16, x + 16);
+                        const float sx = ss[u * lds_ + 2 * j] + ss[u * lds_ + 2 * j + 1];
+                        acc[u] += a * sq + b * sx;
+                    }
+                }
+            }
+        }
+    }
+};
+
+// n consecutive bytes' dwords from a 2-byte-aligned address, realigned: reads the n + 1 aligned dwords around them
+// (from at most 2 bytes before p to at most 4 after p + 4 n).
+template <int N>
+__device__ __forceinline__ void load_words_a2(const uint8_t* p, uint32_t (&out)[N]) {
+    uint32_t sh;
+    const uint32_t* q = align_down4(p, sh);
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) w[i] = q[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+}
+
+template <>
+struct BlockDot<WL_TYPE_Q6_K> {
+    // blk: 2-byte aligned. Value 128 h + 32 t + c: low 4 bits in ql[64 h + 32 (t & 1) + c] (high nibble for t >= 2),
+    // high 2 bits at bit 2 t of qh[32 h + c]; value = (d sc_g) (q6 - 32), g = its 16-value group.
+    // Every read stays within [blk - 2, blk + 210): ql up to byte 132, qh up to 196, scales as 4 dwords from
+    // byte 192 - (blk & 3) and a 16-bit load of bytes 206..207. fetch() issues the loads, run() uses them.
+    uint32_t ql[2][16], qh[2][8], sw[4], d16;
+    __device__ void fetch(const uint8_t* __restrict__ blk) {
+        load_words_a2<16>(blk, ql[0]);
+        load_words_a2<16>(blk + 64, ql[1]);
+        load_words_a2<8>(blk + 128, qh[0]);
+        load_words_a2<8>(blk + 160, qh[1]);
+        uint32_t sh;
+        const uint32_t* q = align_down4(blk + 192, sh);
+        const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
+        const uint32_t tail = *reinterpret_cast<const uint16_t*>(blk + 206);
+        sw[0] = __builtin_amdgcn_alignbyte(w1, w0, sh);
+        sw[1] = __builtin_amdgcn_alignbyte(w2, w1, sh);
+        sw[2] = __builtin_amdgcn_alignbyte(w3, w2, sh);
+        sw[3] = __builtin_amdgcn_alignbyte(tail, w3, sh);
+        d16 = *reinterpret_cast<const uint16_t*>(blk + 208);
+    }
+    __device__ void run(const float* xs, int ldx, const float* ss, int lds_, int n, float (&acc)[kGemvTok]) const {
+        const float d = half_to_float(d16);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int g = 8 * h + 2 * t;  // the two 16-value groups of these 32 values
+                const float a0 = d * static_cast<float>(static_cast<int8_t>((sw[g >> 2] >> (8 * (g & 3))) & 0xFFu));
+                const float a1 =
+                    d * static_cast<float>(static_cast<int8_t>((sw[(g + 1) >> 2] >> (8 * ((g + 1) & 3))) & 0xFFu));
+                const float b0 = -32.0f * a0, b1 = -32.0f * a1;
+                float f[32];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t lo = (ql[h][8 * (t & 1) + i] >> (4 * (t >> 1))) & 0x0F0F0F0Fu;
+                    const uint32_t hi = ((qh[h][i] >> (2 * t)) & 0x03030303u) << 4;
+                    bytes_to_f32(opaque(lo | hi), f + 4 * i);
+                }
+#pragma unroll
+                for (int u = 0; u < kGemvTok; u++) {
+                    if (u < n) {
+                        const float* x = xs + u * ldx + 128 * h + 32 * t;
+                        const float s0 = dot16_lds(f, x), s1 = dot16_lds(f + 16, x + 16);
+                        acc[u] += a0 * s0 + b0 * ss[u * lds_ + g] + a1 * s1 + b1 * ss[u * lds_ + g + 1];
+                    }
+                }
+            }
+        }
+    }
+};
+
+// sum over the L lanes of a row (L a power of two, 1..8)
+template <int L>
+__device__ __forceinline__ float row_sum(float v) {
+    if constexpr (L == 1)
+        return v;
+    else
+        return group_sum<L>(v);
+}
+
+// gate_up + SwiGLU. A wavefront takes JW = 32 / L intermediate rows j: lanes [0, 32) the gate rows j, lanes
+// [32, 64) the up rows inter + j (L lanes per row); a workgroup 4 JW rows. h[pos, j] = silu(gate . x_t) *
+// (up . x_t) for each of the slot's tokens. rows: the intermediate width of every slot of the launch.
+template <int TYPE, int L>
+__global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a, int rows, int chunk) {
+    extern __shared__ __attribute__((aligned(16))) float lds_x[];
+    constexpr int JW = 32 / L, JG = 4 * JW;
+    const int groups = (rows + JG - 1) / JG;
+    const int items = expert_slots(a) * groups;
+    const int lane = threadIdx.x & 63, c = lane % L, rw = (lane & 31) / L;
+    const bool up_half = lane >= 32;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int nb = a.H / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const int ldx = lds_row_floats(a.H), ldsum = a.H / 16;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int slot = it / groups;
+        const ExpertView v = expert_view(a, slot, true);
+        const int inter = static_cast<int>(v.stride_rows);
+        const int j = (it - slot * groups) * JG + wv * JW + rw;
+        const uint8_t* wrow = v.w + static_cast<int64_t>((up_half ? inter : 0) + min(j, inter - 1)) * rs;
+        float* hout = v.routed ? a.h : a.h_sh;
+        BlockDot<TYPE> blk;
+        blk.fetch(wrow + c * BlockInfo<TYPE>::bytes);  // the first block's loads overlap the staging below
+        for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
+            const int n = min(chunk, v.end - p0);
+            __syncthreads();  // the previous chunk's LDS rows are no longer read
+            stage_chunk(lds_x, n, a.H, [&](int u) {
+                const int pos = p0 + u;
+                return a.x + static_cast<int64_t>(v.routed ? a.sorted[pos] / a.k : pos) * a.H;
+            });
+            if ((it - slot * groups) * JG + wv * JW >= inter) continue;  // whole wavefront
+            float acc[kGemvTok];
+#pragma unroll
+            for (int u = 0; u < kGemvTok; u++) acc[u] = 0.0f;
+            for (int kb = c; kb < nb; kb += L) {
+                if (kb != c || p0 != v.begin) blk.fetch(wrow + kb * BlockInfo<TYPE>::bytes);
+                blk.run(lds_x + kb * kBlkFloats, ldx, lds_x + n * ldx + 16 * kb, ldsum, n, acc);
+            }
+#pragma unroll
+            for (int u = 0; u < kGemvTok; u++) {
+                if (u < n) {
+                    const float sum = row_sum<L>(acc[u]);
+                    const float us = __shfl_xor(sum, 32);  // the up row's sum, from the other half
+                    if (!up_half && c == 0 && j < inter)
+                        hout[static_cast<int64_t>(p0 + u) * inter + j] = silu(sum) * us;
+                }
+            }
+        }
+    }
+}
+
+// The down kernel spreads each block of a row over 8 lanes (one 16-byte slice per lane, so a wavefront's weight
+// loads are contiguous) and reads a lane's h runs from LDS once per token for kDnPasses rows. (Lane-per-block
+// loads as in k_gate_up read a 210-byte Q6_K block per lane with strided dword loads: slower for down, measured.)
+// Its LDS rows are padded by 4 floats after every 64 values (lds_padded_index).
+constexpr int kDnPasses = 4;       // down: row passes per wavefront (R rows each)
+__host__ __device__ inline int lds_padded_floats(int width) { return width + 4 * (width / 64); }
+__device__ __forceinline__ int lds_padded_index(int i) { return i + 4 * (i >> 6); }
 
 // Tokens per chunk for rows of `width` values: kGemvTok, or fewer when their LDS copy would pass kGemvLdsMax.
-__host__ inline int gemv_chunk(int width) {
-    const int per = kGemvLdsMax / (4 * lds_row_floats(width));
+__host__ inline int gemv_chunk_padded(int width) {
+    const int per = kGemvLdsMax / (4 * lds_padded_floats(width));
     return per < 1 ? 1 : (per < kGemvTok ? per : kGemvTok);
 }
 
 // rows u < n of the chunk: src_row(u) -> LDS row u (width values, a multiple of 64), 16 bytes per load
 template <typename SrcRow>
-__device__ __forceinline__ void stage_rows(float* lds, int n, int width, SrcRow src_row) {
+__device__ __forceinline__ void stage_padded_rows(float* lds, int n, int width, SrcRow src_row) {
     const int per_row = width / 4;
-    const int ld = lds_row_floats(width);
+    const int ld = lds_padded_floats(width);
     for (int f = threadIdx.x; f < n * per_row; f += blockDim.x) {
         const int u = f / per_row, i = 4 * (f - u * per_row);
-        *reinterpret_cast<float4*>(lds + u * ld + lds_index(i)) =
+        *reinterpret_cast<float4*>(lds + u * ld + lds_padded_index(i)) =
             *reinterpret_cast<const float4*>(src_row(u) + i);
     }
 }
 
 // the lane's 16 values from LDS row u at value offset i (16-aligned: never straddles a padding gap)
-__device__ __forceinline__ void lds_run(const float* lds, int ld, int u, int i, float4 x[4]) {
-    const float4* q = reinterpret_cast<const float4*>(lds + u * ld + lds_index(i));
+__device__ __forceinline__ void lds_padded_run(const float* lds, int ld, int u, int i, float4 x[4]) {
+    const float4* q = reinterpret_cast<const float4*>(lds + u * ld + lds_padded_index(i));
 #pragma unroll
     for (int j = 0; j < 4; j++) x[j] = q[j];
-}
-
-// gate_up + SwiGLU: a row group is 4 kGuRows intermediate rows; wavefront w takes rows j0 .. j0 + kGuRows - 1
-// (gate rows j, up rows inter + j); lane group g takes blocks g, g + 8, ... of each row. With at most 8 blocks per
-// row (hidden <= 2048) a lane holds one block of each of its rows, decoded once for all the chunk's tokens; wider
-// rows are decoded again per token. h[pos, j] = silu(gate . x_t) * (up . x_t). rows: the intermediate width of
-// every slot of the launch.
-template <int TYPE>
-__global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a, int rows, int chunk) {
-    extern __shared__ __attribute__((aligned(16))) float lds_x[];
-    constexpr int kRowsPerGroup = 4 * kGuRows;
-    const int groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
-    const int items = expert_slots(a) * groups;
-    const int lane = threadIdx.x & 63, g = lane >> 3, c = lane & 7;
-    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int nb = a.H / kQK;
-    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
-    const int lo_start = BlockInfo<TYPE>::lo_start(c), hi_off = BlockInfo<TYPE>::hi_offset;
-    const int ld = lds_row_floats(a.H);
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
-        const int slot = it / groups;
-        const ExpertView v = expert_view(a, slot, true);
-        const int inter = static_cast<int>(v.stride_rows);
-        const int j0 = (it - slot * groups) * kRowsPerGroup + wv * kGuRows;
-        float* hout = v.routed ? a.h : a.h_sh;
-        // the lane's weights of block kb for the wavefront's rows (rows past inter load row inter - 1, never stored)
-        Lane32 wg[kGuRows], wu[kGuRows];
-        auto decode_rows = [&](int kb) {
-            RawLane<TYPE> rg[kGuRows], ru[kGuRows];
-#pragma unroll
-            for (int r = 0; r < kGuRows; r++) {
-                const int j = min(j0 + r, inter - 1);
-                rg[r].fetch(v.w + static_cast<int64_t>(j) * rs + kb * BlockInfo<TYPE>::bytes, c);
-                ru[r].fetch(v.w + static_cast<int64_t>(inter + j) * rs + kb * BlockInfo<TYPE>::bytes, c);
-            }
-#pragma unroll
-            for (int r = 0; r < kGuRows; r++) {
-                rg[r].unpack(c, wg[r]);
-                ru[r].unpack(c, wu[r]);
-            }
-        };
-        const bool one_block = nb <= 8;
-        if (one_block && g < nb && j0 < inter) decode_rows(g);  // issued before the x staging waits
-        for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
-            const int n = min(chunk, v.end - p0);
-            __syncthreads();  // the previous chunk's LDS rows are no longer read
-            stage_rows(lds_x, n, a.H, [&](int u) {
-                const int pos = p0 + u;
-                return a.x + static_cast<int64_t>(v.routed ? a.sorted[pos] / a.k : pos) * a.H;
-            });
-            __syncthreads();
-            if (j0 >= inter) continue;  // whole wavefront (it still takes part in the barriers)
-#pragma unroll 1
-            for (int u = 0; u < n; u++) {
-                float ag[kGuRows], au[kGuRows];
-#pragma unroll
-                for (int r = 0; r < kGuRows; r++) ag[r] = au[r] = 0.0f;
-                for (int kb = g; kb < nb; kb += 8) {
-                    if (!one_block) decode_rows(kb);
-                    float4 xl[4], xh[4];
-                    lds_run(lds_x, ld, u, kb * kQK + lo_start, xl);
-                    lds_run(lds_x, ld, u, kb * kQK + lo_start + hi_off, xh);
-                    const float sxl = sum16(xl), sxh = sum16(xh);
-#pragma unroll
-                    for (int r = 0; r < kGuRows; r++) {
-                        ag[r] += lane_dot_s(wg[r], xl, xh, sxl, sxh);
-                        au[r] += lane_dot_s(wu[r], xl, xh, sxl, sxh);
-                    }
-                }
-                const int64_t row = p0 + u;  // routed: sorted position; shared: token
-#pragma unroll
-                for (int r = 0; r < kGuRows; r++) {
-                    const float gs = group_sum<64>(ag[r]);
-                    const float us = group_sum<64>(au[r]);
-                    if (lane == 0 && j0 + r < inter) hout[row * inter + j0 + r] = silu(gs) * us;
-                }
-            }
-        }
-    }
 }
 
 // down: a row group is 4 wavefronts x kDnPasses passes x R output rows (R = 64 / WIDTH, WIDTH = 8 nb lanes per
@@ -587,7 +747,7 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a, int chunk) {
         const ExpertView v = expert_view(a, slot, false);
         const int inter = static_cast<int>(v.stride_rows);
         const int nb = inter / kQK;
-        const int ld = lds_row_floats(inter);
+        const int ld = lds_padded_floats(inter);
         const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
         const int row_off = R > 1 ? g / nb : 0;
         const int kb0 = R > 1 ? g % nb : g;
@@ -612,7 +772,7 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a, int chunk) {
         for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
             const int n = min(chunk, v.end - p0);
             __syncthreads();
-            stage_rows(lds_h, n, inter, [&](int u) { return hin + static_cast<int64_t>(p0 + u) * inter; });
+            stage_padded_rows(lds_h, n, inter, [&](int u) { return hin + static_cast<int64_t>(p0 + u) * inter; });
             __syncthreads();
             if (wave_row0 >= a.H) continue;  // whole wavefront
 #pragma unroll 1
@@ -624,8 +784,8 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a, int chunk) {
                     for (int kb = kb0; kb < nb; kb += kb_step) {
                         if (!one_block) decode_rows(kb);
                         float4 xl[4], xh[4];
-                        lds_run(lds_h, ld, u, kb * kQK + lo_start, xl);
-                        lds_run(lds_h, ld, u, kb * kQK + lo_start + hi_off, xh);
+                        lds_padded_run(lds_h, ld, u, kb * kQK + lo_start, xl);
+                        lds_padded_run(lds_h, ld, u, kb * kQK + lo_start + hi_off, xh);
                         const float sxl = sum16(xl), sxh = sum16(xh);
 #pragma unroll
                         for (int q = 0; q < kDnPasses; q++) acc[q] += lane_dot_s(w[q], xl, xh, sxl, sxh);
@@ -890,11 +1050,22 @@ static unsigned gemv_grid(int64_t items) {
     return static_cast<unsigned>(items < kMaxGroups ? (items > 0 ? items : 1) : kMaxGroups);
 }
 
+template <int TYPE, int L>
+static void launch_gate_up_l(const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
+    constexpr int JG = 4 * (32 / L);
+    const unsigned grid = gemv_grid(static_cast<int64_t>(max_slots) * ((rows + JG - 1) / JG));
+    const int chunk = gemv_chunk(a.H);
+    k_gate_up<TYPE, L><<<grid, 256, sizeof(float) * chunk * lds_chunk_floats(a.H), s>>>(a, rows, chunk);
+}
+
 template <int TYPE>
 static void launch_gate_up_t(const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
-    const unsigned grid = gemv_grid(static_cast<int64_t>(max_slots) * ((rows + 4 * kGuRows - 1) / (4 * kGuRows)));
-    const int chunk = gemv_chunk(a.H);
-    k_gate_up<TYPE><<<grid, 256, sizeof(float) * chunk * lds_row_floats(a.H), s>>>(a, rows, chunk);
+    switch (gemv_lanes(a.H / kQK)) {
+        case 1: launch_gate_up_l<TYPE, 1>(a, rows, max_slots, s); break;
+        case 2: launch_gate_up_l<TYPE, 2>(a, rows, max_slots, s); break;
+        case 4: launch_gate_up_l<TYPE, 4>(a, rows, max_slots, s); break;
+        default: launch_gate_up_l<TYPE, 8>(a, rows, max_slots, s); break;
+    }
 }
 
 static void launch_gate_up(int type, const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
@@ -909,8 +1080,8 @@ static void launch_down_w(const ExpertArgs& a, int inter, int max_slots, hipStre
     constexpr int R = WIDTH == 64 ? 1 : 64 / WIDTH;
     const unsigned grid =
         gemv_grid(static_cast<int64_t>(max_slots) * ((a.H + 4 * R * kDnPasses - 1) / (4 * R * kDnPasses)));
-    const int chunk = gemv_chunk(inter);
-    k_down<TYPE, WIDTH><<<grid, 256, sizeof(float) * chunk * lds_row_floats(inter), s>>>(a, chunk);
+    const int chunk = gemv_chunk_padded(inter);
+    k_down<TYPE, WIDTH><<<grid, 256, sizeof(float) * chunk * lds_padded_floats(inter), s>>>(a, chunk);
 }
 
 template <int TYPE>
