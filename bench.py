@@ -278,6 +278,8 @@ def main():
     ap.add_argument("--skip-linear", action="store_true")
     ap.add_argument("--load-layers", type=int, default=8,
                     help="full-shape layers in the synthetic GGUF file of the loader measurement")
+    ap.add_argument("--no-next", action="store_true",
+                    help="decode without the next-layer overlap (WlMoeLayer.next unset)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode layers eagerly instead of replaying HIP graphs (for counter runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -305,6 +307,9 @@ def main():
     log(f"building {args.layers} layers in HBM")
     t = time.time()
     layers = build_layers(torch, hip, args.layers)
+    if not args.no_next:  # each layer names the one run after it (the step loops back to layer 0)
+        for i, layer in enumerate(layers):
+            layer.set_next(layers[(i + 1) % len(layers)])
     torch.cuda.synchronize()
     log(f"built in {time.time() - t:.1f}s, {torch.cuda.memory_allocated() / 1e9:.1f} GB allocated")
 

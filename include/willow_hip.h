@@ -106,6 +106,12 @@ typedef struct WlMoeLayer {
     int32_t n_experts, top_k, norm_topk_prob;
     int32_t flags;               /* WL_MOE_* bits; 0 = defaults */
     int32_t reserved;            /* 0 */
+    /* The layer the caller runs next, or NULL. When it has the same shapes and types, the batch-1 fused kernel
+     * pulls the rows that the next layer's first phase reads whatever the routing (its router rows and shared
+     * expert rows) into the GPU's caches while this layer waits on its own exchanges: the next-layer overlap that
+     * the reference's guess_next_layer provides for its SSD reads (engines/base.py:392-406). Only read, never
+     * written; it must stay valid until the call's work has run. */
+    const struct WlMoeLayer* next;
 } WlMoeLayer;
 
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout():
     assert hip.library().wl_abi_version() >> 16 == 1
-    assert ctypes.sizeof(hip.WlMoeLayer) == 7 * 8 + 2 * 8 + 12 * 4
+    assert ctypes.sizeof(hip.WlMoeLayer) == 7 * 8 + 2 * 8 + 12 * 4 + 8
 
 
 def test_error_strings():

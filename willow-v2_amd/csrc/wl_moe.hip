@@ -961,7 +961,15 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     return w;
 }
 
+static int check_one_layer(const WlMoeLayer* L);
+
 int check_layer(const WlMoeLayer* L) {
+    const int rc = check_one_layer(L);
+    if (rc || !L->next) return rc;
+    return check_one_layer(L->next);  // only its own fields; its next is not followed
+}
+
+static int check_one_layer(const WlMoeLayer* L) {
     if (!L) return WL_EINVAL_NULL;
     if (!L->gate_up || !L->down || !L->router) return WL_EINVAL_NULL;
     if (block_bytes(L->gate_up_type) < 0 || block_bytes(L->down_type) < 0) return WL_EINVAL_TYPE;
@@ -1190,7 +1198,7 @@ const char* wl_error_string(int code) {
     return "unknown error";
 }
 
-int wl_abi_version(void) { return (1 << 16) | 1; }  // 1.1: wl_linear
+int wl_abi_version(void) { return (1 << 16) | 2; }  // 1.2: WlMoeLayer.next, wl_moe_layer_noalloc, status
 
 int wl_moe_check(const WlMoeLayer* layer) { return check_layer(layer); }
 

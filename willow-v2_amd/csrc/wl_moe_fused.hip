@@ -70,7 +70,27 @@ struct FusedArgs {
     int H, I, E, k, renorm, G;
     uint32_t spin_limit;  // polls before a wait gives up
     int silent_wg;        // WL_MOE_TEST_STARVE: this workgroup publishes nothing (-1: none)
+    // the next layer's rows read before its routing is known (NULL next_router: no prefetch); same shapes
+    const float* next_router;
+    const float* next_sh_gate;
+    const uint8_t* next_sh_gate_up;
+    const uint8_t* next_sh_down;
 };
+
+// The 128-byte lines of what wavefront slot t reads in phase A (router row t, or the shared expert's gate row j and
+// up row I + j for t = n_router + j), and of an owner workgroup's shared down rows: lane l touches line l of the
+// wavefront's share (one dword each), so the lines come into this XCD's L2 (and the memory-side cache) ahead of
+// the next layer's phase A, which runs the same task on the same workgroup and wavefront.
+__device__ __forceinline__ uint32_t touch_lines(const uint8_t* base, int bytes, int lane) {
+    const int lines = (bytes + 127) / 128 + 1;  // +1: the rows need not start on a line
+    uint32_t v = 0;
+    if (lane < lines && base) {
+        const uint8_t* p = base + 128 * lane;
+        if (lane == lines - 1) p = base + bytes - 4;  // the last line, without reading past the rows
+        v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t{3});
+    }
+    return v;
+}
 
 __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32_t tag, float v) {
     const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
@@ -410,6 +430,25 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // down: wavefront s < k takes the owner's rows of the s-th picked expert. They are requested only now (so far
     // the gate_up rows had the bandwidth and the load queues to themselves) and arrive while h crosses workgroups;
     // then the wavefront gathers that expert's h, dots its 8 rows and leaves the sums in LDS
+    // next-layer overlap: the lines this wavefront's phase A task reads in the next layer (and, in the last
+    // wavefront, the next layer's shared down rows of this owner), requested now: this wavefront's first h poll
+    // below would not succeed before they arrive anyway. Consumed (never used) at the very end.
+    uint32_t touched = 0;
+    if (a.next_router) {
+        const int t = slot;
+        if (t < n_router) {
+            const float* wr = t < E ? a.next_router + static_cast<int64_t>(t) * H : a.next_sh_gate;
+            touched = touch_lines(reinterpret_cast<const uint8_t*>(wr), 4 * H, lane);
+        } else if (t < n_a) {
+            const int j = t - n_router;
+            const int part = lane >> 5;  // lanes 0..31 the gate row, 32..63 the up row
+            touched = touch_lines(a.next_sh_gate_up + static_cast<int64_t>(part ? I + j : j) * gu_rs,
+                                  static_cast<int>(gu_rs), lane & 31);
+        }
+        if (wv == kFusedWaves - 1 && owner && a.next_sh_down)
+            touched ^= touch_lines(a.next_sh_down + static_cast<int64_t>(kOwnRows * b) * dn_rs,
+                                   static_cast<int>(kOwnRows * dn_rs), lane);
+    }
     if (owner && wv < k) {
         auto own_row = [&](int pass) { return kOwnRows * b + R * pass + drow; };
         RawLane<DN> draw[NBD];
@@ -448,6 +487,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     }
     if (!all_ok && threadIdx.x == 0)  // a vector atomic, visible to the host's status query
         __hip_atomic_fetch_or(a.sync + kStatusWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __asm__ volatile("" ::"v"(touched));  // the prefetch loads count as used, so they are kept
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -554,6 +594,19 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
     const bool starve = (L.flags & WL_MOE_TEST_STARVE) != 0;
     a.spin_limit = starve ? kStarveSpinLimit : kSpinLimit;
     a.silent_wg = starve ? a.G - 1 : -1;
+    const WlMoeLayer* nx = L.next;
+    // the next layer's phase A maps tasks to workgroups and wavefronts the same way only with the same shapes
+    if (nx && nx->hidden == L.hidden && nx->n_experts == L.n_experts && nx->inter == L.inter &&
+        nx->top_k == L.top_k && nx->gate_up_type == L.gate_up_type && nx->down_type == L.down_type &&
+        (nx->shared_gate_up != nullptr) == (L.shared_gate_up != nullptr) &&
+        (!L.shared_gate_up || (nx->shared_inter == L.shared_inter && nx->shared_gate_up_type == L.shared_gate_up_type &&
+                               nx->shared_down_type == L.shared_down_type &&
+                               (nx->shared_gate != nullptr) == (L.shared_gate != nullptr)))) {
+        a.next_router = nx->router;
+        a.next_sh_gate = nx->shared_gate_up ? nx->shared_gate : nullptr;
+        a.next_sh_gate_up = static_cast<const uint8_t*>(nx->shared_gate_up);
+        a.next_sh_down = static_cast<const uint8_t*>(nx->shared_down);
+    }
     void* args[] = {&a};
     const hipError_t e = hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a.G)), dim3(kFusedThreads), args, 0, s);
     return e == hipSuccess ? WL_OK : static_cast<int>(e);

@@ -9,8 +9,10 @@ moe(x, layer, residual) keeps the layer API called at engines/qwen36/model.py:22
 device in, the same shape and dtype out. It reads the same attributes and weight names as the reference
 (self.prefix, self.top_k, self.norm_topk_prob; <prefix>layers.N.mlp.{gate, shared_expert.{gate,up,down}_proj,
 shared_expert_gate}.weight; engines/base.py:285-286,446,481-485) and runs the router, top-k, grouping, experts and
-combine on the GPU in one call: no `selected.cpu()` wait per layer (engines/base.py:456-460), no guess of the next
-layer's experts (nothing to prefetch), no per-expert launches.
+combine on the GPU in one call: no `selected.cpu()` wait per layer (engines/base.py:456-460) and no per-expert
+launches. In place of guess_next_layer (engines/base.py:392-406), which guesses the next layer's experts to start
+their SSD reads, each layer's view names the next layer, and a batch-1 call pulls the next layer's router and
+shared-expert rows (read before its routing is known) into the GPU's caches while it waits on its own exchanges.
 
 Shared expert: when its three matrices are GGMLWeight (kept quantized), they run inside the fused kernel; when
 they are dense tensors (the reference's loader dequantizes them to bf16, engines/qwen36/loader.py:224), the
@@ -69,6 +71,11 @@ class HipMoE:
 
     def moe(self, x: torch.Tensor, layer: int, residual: torch.Tensor = None) -> torch.Tensor:
         view, dense = self.hip_layer(layer)
+        nxt = layer + 1
+        if getattr(view, "_next", None) is None and nxt < len(getattr(self.experts, "layers", ())):
+            # the next layer's router and shared-expert rows are pulled into the caches during this layer
+            # (the overlap guess_next_layer gives the reference's SSD reads, engines/base.py:392-406)
+            view.set_next(self.hip_layer(nxt)[0])
         flat = x.reshape(-1, x.shape[-1])
         out = view(flat.to(view.device))
         if dense is not None:

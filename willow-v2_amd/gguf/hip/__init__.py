@@ -45,6 +45,7 @@ class WlMoeLayer(ctypes.Structure):
         ("shared_down_type", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
         ("shared_inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("top_k", ctypes.c_int32),
         ("norm_topk_prob", ctypes.c_int32), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("next", ctypes.c_void_p),
     ]
 
 

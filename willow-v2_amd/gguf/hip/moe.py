@@ -82,6 +82,14 @@ class MoELayer:
                    shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"),
                    fused=fused, mfma=mfma)
 
+    def set_next(self, layer: "MoELayer" = None):
+        """The layer the caller runs after this one (or None). With the same shapes, a batch-1 call pulls the rows
+        that layer reads before its routing is known (router, shared expert) into the GPU's caches while this
+        layer waits on its exchanges (WlMoeLayer.next). `layer` is kept alive by this one."""
+        self._next = layer
+        self.struct.next = None if layer is None else ctypes.addressof(layer.struct)
+        check(library().wl_moe_check(ctypes.byref(self.struct)))
+
     def workspace_bytes(self, tokens: int) -> int:
         return int(library().wl_moe_workspace_bytes(ctypes.byref(self.struct), tokens))
 
