@@ -44,6 +44,7 @@ extern "C" {
 #define WL_EINVAL_COUNT -8     /* too many experts for one batched call */
 #define WL_EINVAL_SCRATCH -9   /* wl_moe_layer_noalloc: the call needs more than WL_NOALLOC_SCRATCH_BYTES */
 #define WL_ESYNC -10           /* wl_moe_workspace_status: a fused-kernel wait gave up since the last query */
+#define WL_EINVAL_OVERLAP -11  /* wl_moe_layer: y overlaps x */
 
 #define WL_MAX_TOPK 16
 #define WL_MAX_BATCH_EXPERTS 64 /* experts per wl_gemv_batch / wl_gemv_combine call */
@@ -112,11 +113,22 @@ typedef struct WlMoeLayer {
      * the reference's guess_next_layer provides for its SSD reads (engines/base.py:392-406). Only read, never
      * written; it must stay valid until the call's work has run. */
     const struct WlMoeLayer* next;
+    /* With WL_MOE_PRE_NORM in flags: the layer runs on rms_norm(x) instead of x, as the reference's zero-centered
+     * RMSNorm computes it (engines/base.py:27-31: x * rsqrt(mean(x^2) + eps) * (1 + w)), in this fixed fp32 order:
+     * s = sum of x_i^2 in the router's order (64-value segments, each a chain of fused multiply-adds from 0 in
+     * ascending i, the segments added left to right), inv = 1 / sqrt(s / hidden + eps) (each step rounded once),
+     * x_i * inv * (1 + w_i) (rounded after each product; w = 0 when norm_weight is NULL). */
+    const float* norm_weight;    /* fp32 [hidden] (post_attention_layernorm.weight) or NULL */
+    float norm_eps;
+    int32_t reserved2;           /* 0 */
 } WlMoeLayer;
 
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */
 #define WL_MOE_NO_MFMA 2         /* flags: every expert on the fp32 GEMV kernels at any token count */
 #define WL_MOE_FORCE_MFMA 4      /* flags: every expert on the bf16 MFMA GEMMs at any token count (testing) */
+#define WL_MOE_PRE_NORM 16       /* flags: run on rms_norm(x) (norm_weight, norm_eps; see WlMoeLayer) */
+#define WL_MOE_RESIDUAL 32       /* flags: y = x + MoE(input), the residual add of engines/qwen36/model.py:22; y and
+                                    x must not overlap */
 #define WL_MOE_TEST_STARVE 8     /* flags, testing only: in the fused kernel one workgroup withholds its results and
                                     the others' bounded waits give up early, so the call ends with NaN outputs and
                                     the workspace's status word set (the failure wl_moe_workspace_status reports) */

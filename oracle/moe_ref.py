@@ -132,6 +132,22 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, chain: str = "fp32", return
     return y
 
 
+def rms_norm(x: np.ndarray, weight=None, eps: float = 1e-6) -> np.ndarray:
+    """engines/base.py:27-31 with zero_centered (x * rsqrt(mean(x^2) + eps) * (1 + w); Qwen3.5's norm,
+    engines/qwen36/model.py:37) in the layer's fixed fp32 order: the sum of squares in the router's order
+    (cref.router_logits of x with itself), then mean = s / H, inv = 1 / sqrt(mean + eps), x * inv * (1 + w), every
+    step a correctly rounded float32 operation."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    ss = np.array([cref.router_logits(x[t:t + 1], x[t:t + 1])[0, 0] for t in range(T)], dtype=np.float32)
+    mean = ss / np.float32(H)
+    inv = np.float32(1.0) / np.sqrt(mean + np.float32(eps))
+    out = x * inv[:, None]
+    if weight is not None:
+        out = out * (np.float32(1.0) + np.asarray(weight, dtype=np.float32))
+    return out.astype(np.float32)
+
+
 def topk_margins(logits: np.ndarray, top_k: int) -> np.ndarray:
     """Per token, the gap between its top_k-th and (top_k + 1)-th largest logit: how far the selection is from a
     tie (a gap of 0 is a tie, broken toward the lower expert id)."""

@@ -27,12 +27,13 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout():
     assert hip.library().wl_abi_version() >> 16 == 1
-    assert ctypes.sizeof(hip.WlMoeLayer) == 7 * 8 + 2 * 8 + 12 * 4 + 8
+    # 7 weight pointers, 2 shared-expert pointers, 12 int32 fields, next, norm_weight, norm_eps + reserved2
+    assert ctypes.sizeof(hip.WlMoeLayer) == 7 * 8 + 2 * 8 + 12 * 4 + 8 + 8 + 8 == 144
 
 
 def test_error_strings():
     lib = hip.library()
-    for code in range(-9, 1):
+    for code in range(-11, 1):
         assert lib.wl_error_string(code)
     assert b"unsupported" in lib.wl_error_string(-1)
 
@@ -115,7 +116,7 @@ def test_layer_validation(over, code):
     if code == 0:
         assert lib.wl_moe_workspace_bytes(ctypes.byref(s), 1) > 0
         assert lib.wl_moe_workspace_bytes(ctypes.byref(s), 64) > lib.wl_moe_workspace_bytes(ctypes.byref(s), 1)
-        assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 1, FAKE, None, None, None, 0, None) == -6
+        assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 1, FAKE + (1 << 24), None, None, None, 0, None) == -6
         assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 0, FAKE, None, None, FAKE, 1 << 30, None) == -2
     else:
         assert lib.wl_moe_workspace_bytes(ctypes.byref(s), 1) == 0
@@ -149,3 +150,31 @@ def test_noalloc_validation_without_a_gpu():
     assert lib.wl_moe_layer_noalloc(ctypes.byref(s), None, 1, FAKE, None, None, None) == -3
     s.top_k = 0
     assert lib.wl_moe_layer_noalloc(ctypes.byref(s), FAKE, 1, FAKE, None, None, None) == -5
+
+
+def test_norm_residual_validation_without_a_gpu():
+    """wl_moe_layer rejects y overlapping x, and a pre-norm layer with a negative eps or a misaligned weight, before
+    it touches the device."""
+    lib = hip.library()
+    s = hip.WlMoeLayer()
+    s.gate_up = s.down = s.router = s.shared_gate_up = s.shared_down = s.shared_gate = FAKE
+    s.gate_up_stride, s.down_stride = 1179648, 860160
+    s.gate_up_type = s.shared_gate_up_type = 12
+    s.down_type = s.shared_down_type = 14
+    s.hidden, s.inter, s.shared_inter, s.n_experts, s.top_k, s.norm_topk_prob = 2048, 512, 512, 256, 8, 1
+    s.flags = hip.MOE_RESIDUAL
+    ws = ctypes.c_void_p(FAKE)
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 2, FAKE, None, None, ws, 0, None) == -11
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 2, FAKE + 2048 * 4, None, None, ws, 0, None) == -11
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 2, FAKE + 2 * 2048 * 4, None, None, ws, 0, None) == -6
+    s.flags = hip.MOE_PRE_NORM
+    s.norm_eps = -1.0
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 1, FAKE + 2048 * 4, None, None, ws, 0, None) == -2
+    s.norm_eps = float("nan")
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 1, FAKE + 2048 * 4, None, None, ws, 0, None) == -2
+    s.norm_eps, s.norm_weight = 1e-6, FAKE + 4
+    assert lib.wl_moe_layer(ctypes.byref(s), FAKE, 1, FAKE + 2048 * 4, None, None, ws, 0, None) == -2
+    s.norm_weight = FAKE
+    with_norm = lib.wl_moe_workspace_bytes(ctypes.byref(s), 4)
+    s.flags = 0
+    assert with_norm - lib.wl_moe_workspace_bytes(ctypes.byref(s), 4) >= 4 * 2048 * 4  # the normalized input

@@ -61,7 +61,7 @@ def test_engine_moe_matches_oracle(small_layer, quantized_shared, tokens):
     y = eng.moe(torch.from_numpy(x).cuda(), 0, residual=None)
     assert y.shape == (tokens, 2048) and y.dtype == torch.float32
     # each expert by its own token count; a dense shared expert runs in torch on its fp32 weights
-    ref = moe_ref.layer(x, lw, chain="split", shared_chain=None if quantized_shared else "fp32")
+    ref = moe_ref.layer(x, lw, chain="split", shared_chain=None if quantized_shared else "fp32", dtype=np.float64)
     assert moe_ref.rel_err(y.cpu().numpy(), ref) < 2e-3
     yb = eng.moe(torch.from_numpy(x).cuda().to(torch.bfloat16), 0)
     assert yb.dtype == torch.bfloat16

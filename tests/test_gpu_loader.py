@@ -60,5 +60,5 @@ def test_loaded_model_runs(model, layer, tokens):
     eng = TinyEngine(store, weights, cfg)
     x = synth.tokens(80 + tokens, tokens)
     y = eng.moe(torch.from_numpy(x).cuda(), layer).cpu().numpy()
-    ref = moe_ref.layer(x, layers[layer], chain="split")  # each expert by its own token count
+    ref = moe_ref.layer(x, layers[layer], chain="split", dtype=np.float64)  # each expert by its own count
     assert moe_ref.rel_err(y, ref) < 2e-3

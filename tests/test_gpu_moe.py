@@ -195,11 +195,14 @@ def test_layer_variants(hip, variant):
 def check_prefill(hip, layer, lw, x, label, tol=TOL):
     """A plan with MFMA experts against the oracle's chain for that plan ("split": the reference's per-expert
     rule; "mfma": every expert on the bf16 chain of engines/base.py:568-570 with bf16 tensors), and against the
-    all-fp32 oracle within bf16 accuracy."""
+    all-fp32 oracle within bf16 accuracy. The chain oracle accumulates in float64, so each bf16 rounding applies to
+    the exactly rounded fp32 sum: with numpy's own fp32 summation order the oracle's output can sit one bf16 ulp
+    (3.9e-3 relative) away from the exact chain at a token whose value lies on a rounding boundary, a flip no
+    accumulation order is entitled to more than another."""
     chain = {"split": "split", "mfma": "bf16"}[layer.plan(x.shape[0])]
     print(f"[prefill] {label}: T={x.shape[0]} chain={chain}", flush=True)
     y, ids, wts = run_layer(hip, layer, x)
-    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, chain=chain, return_routing=True)
+    y_b, ids_ref, wts_ref, _ = moe_ref.layer(x, lw, chain=chain, return_routing=True, dtype=np.float64)
     np.testing.assert_array_equal(ids, ids_ref)
     np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
     err = moe_ref.rel_err(y, y_b)
@@ -230,7 +233,7 @@ def test_prefill_full_chunk_sampled(hip, c2, layer_c2):
     np.testing.assert_allclose(wts, wts_ref, rtol=2e-6, atol=1e-7)
     pick = np.sort(np.random.default_rng(5).choice(T, 24, replace=False))
     counts = np.bincount(ids_ref.reshape(-1), minlength=layer_c2["experts"])
-    y_ref = moe_ref.layer(x[pick], layer_c2, chain="split", counts=counts, layer_tokens=T)
+    y_ref = moe_ref.layer(x[pick], layer_c2, chain="split", counts=counts, layer_tokens=T, dtype=np.float64)
     err = moe_ref.rel_err(y[pick], y_ref)
     print(f"[prefill] full chunk T=4096, 24 sampled tokens: rel err {err:.2e}", flush=True)
     assert err < TOL
@@ -274,3 +277,29 @@ def test_fused_give_up_is_reported(hip, layer_c2):
     assert layer.status(ws) == 0
     assert np.isfinite(y).all()
     assert moe_ref.rel_err(y, moe_ref.layer(x, layer_c2)) < TOL
+
+
+@pytest.fixture(scope="module")
+def c2_norm_weight():
+    return (np.random.default_rng(5).standard_normal(2048) * 0.1).astype(np.float32)
+
+
+@pytest.mark.parametrize("T,weighted,residual", [(1, True, True), (1, False, False), (1, True, False),
+                                                   (9, True, True), (64, True, True), (64, False, False)])
+def test_pre_norm_residual(hip, c2, layer_c2, c2_norm_weight, T, weighted, residual):
+    """WL_MOE_PRE_NORM / WL_MOE_RESIDUAL (one decoder step's x + MoE(rms_norm(x)), engines/qwen36/model.py:22) at
+    batch 1 (fused kernel) and 9, 64 (multi-kernel GEMV / split plans). The normalization is bit-exact with the
+    oracle's fixed-order rms_norm, so the flagged layer on x equals, bit for bit, x + the plain layer on the oracle's
+    rms_norm(x); the plain layer on that input is checked against the oracle."""
+    w = c2_norm_weight if weighted else None
+    layer = hip.MoELayer.from_host(layer_c2, pre_norm=True, norm_weight=w, norm_eps=1e-6, residual=residual)
+    x = synth.tokens(6, T) * np.float32(3.0)  # off unit scale, so a dropped normalization cannot pass
+    xn = moe_ref.rms_norm(x, w, 1e-6)
+    print(f"[moe] pre_norm T={T} weighted={weighted} residual={residual} plan={layer.plan(T)}", flush=True)
+    y, ids, wts = run_layer(hip, layer, x)
+    y_plain, ids_plain, wts_plain = run_layer(hip, c2, xn)
+    np.testing.assert_array_equal(ids, ids_plain)
+    np.testing.assert_array_equal(wts.view(np.uint32), wts_plain.view(np.uint32))
+    want = (x + y_plain) if residual else y_plain
+    np.testing.assert_array_equal(y.view(np.uint32), want.view(np.uint32))
+    check_layer(hip, c2, layer_c2, xn, f"pre_norm T={T}")

@@ -202,3 +202,37 @@ def test_layer_matches_transformers_block():
         theirs = block(torch.from_numpy(x)[None])[0].numpy()
     ours = moe_ref.layer(x, lw)
     assert moe_ref.rel_err(ours, theirs) < 1e-5
+
+
+def test_rms_norm_oracle():
+    """The oracle's RMSNorm against the reference's formula in torch (engines/base.py:27-31, zero-centered) within
+    a few ulps (torch's rsqrt is not correctly rounded), against float64, and its sum of squares in the router's
+    order against exact rational arithmetic on a short row."""
+    import torch
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((6, 512)) * np.array([1, 10, 1e-3, 1e3, 1, 1])[:, None]).astype(np.float32)
+    w = (rng.standard_normal(512) * 0.1).astype(np.float32)
+    ours = moe_ref.rms_norm(x, w, 1e-6)
+    xt = torch.from_numpy(x)
+    theirs = (xt * torch.rsqrt(xt.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + torch.from_numpy(w))).numpy()
+    np.testing.assert_allclose(ours, theirs, rtol=4e-7, atol=0)
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-6) * (1 + w.astype(np.float64))
+    np.testing.assert_allclose(ours, exact, rtol=1e-6)
+    assert np.array_equal(moe_ref.rms_norm(x, None, 1e-6), moe_ref.rms_norm(x, np.zeros(512, np.float32), 1e-6))
+    from fractions import Fraction
+    short = x[:1, :128]
+    ss = cref.router_logits(short, short)[0, 0]
+    # the replayed order: two 64-value fused multiply-add chains (each step rounded once), then their sum
+    def fma_chain(v):
+        acc = np.float32(0)
+        for e in v:
+            acc = np.float32(Fraction(float(acc)) + Fraction(float(e)) * Fraction(float(e)))
+        return acc
+    assert ss == np.float32(fma_chain(short[0, :64]) + fma_chain(short[0, 64:]))
+
+
+def test_topk_margins():
+    logits = np.array([[5, 4, 3, 2, 1, 0], [1, 1, 1, 1, 1, 1], [0, 3, 9, 3, 2, 8]], dtype=np.float32)
+    np.testing.assert_array_equal(moe_ref.topk_margins(logits, 2), [1, 0, 5])
+    np.testing.assert_array_equal(moe_ref.topk_margins(logits, 3), [1, 0, 0])

@@ -112,6 +112,7 @@ struct Workspace {
     int32_t* n_tiles;   // [2]: gate_up tiles, down tiles
     uint16_t* h16;      // [T*k, inter] bf16
     uint16_t* h_sh16;   // [T, shared_inter] bf16
+    float* xn;          // [T, hidden] the normalized input (WL_MOE_PRE_NORM)
     size_t bytes;
 };
 

@@ -151,6 +151,20 @@ __global__ __launch_bounds__(64) void k_router1(const float* __restrict__ x, con
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// The layer's input as RMSNorm of x (WL_MOE_PRE_NORM), one wavefront per token, in the fixed order the layer
+// documents (the fused decode kernel applies the same NormX as it loads x): xn[t] = x[t] * inv * (1 + w).
+__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, const float* __restrict__ w, float eps,
+                                                 int T, int H, float* __restrict__ xn) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float* xt = x + static_cast<int64_t>(t) * H;
+    const NormX nx{xt, w, norm_inv(router_row(xt, xt, true, H, lane), H, eps)};
+    float4* out = reinterpret_cast<float4*>(xn + static_cast<int64_t>(t) * H);
+    for (int i = lane; i < H / 4; i += 64) out[i] = nx(i);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Top-k: one wavefront per token (wave_topk). corder[t, i] = the slot of the token's i-th smallest expert id, the
 // order the combine adds experts in.
 template <int EJ>
@@ -837,7 +851,7 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
                                                  const int32_t* __restrict__ pair_pos,
                                                  const float* __restrict__ wts, const float* __restrict__ o,
                                                  const SH* __restrict__ o_sh, const float* __restrict__ sg,
-                                                 float* __restrict__ y) {
+                                                 const float* __restrict__ resid, float* __restrict__ y) {
     const int spans = (H + kCombineSpan - 1) / kCombineSpan;
     const int t = static_cast<int>(blockIdx.x) / spans;
     const int r = (static_cast<int>(blockIdx.x) - t * spans) * kCombineSpan + 8 * static_cast<int>(threadIdx.x);
@@ -910,6 +924,13 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
         a1.z += gv * sv.b.z;
         a1.w += gv * sv.b.w;
     }
+    if (resid) {  // y = x + MoE (WL_MOE_RESIDUAL)
+        const Float8 xv = load8(resid + static_cast<int64_t>(t) * H + r);
+        a0 = make_float4(__fadd_rn(xv.a.x, a0.x), __fadd_rn(xv.a.y, a0.y), __fadd_rn(xv.a.z, a0.z),
+                         __fadd_rn(xv.a.w, a0.w));
+        a1 = make_float4(__fadd_rn(xv.b.x, a1.x), __fadd_rn(xv.b.y, a1.y), __fadd_rn(xv.b.z, a1.z),
+                         __fadd_rn(xv.b.w, a1.w));
+    }
     float* out = y + static_cast<int64_t>(t) * H + r;
     *reinterpret_cast<float4*>(out) = a0;
     *reinterpret_cast<float4*>(out + 4) = a1;
@@ -957,6 +978,7 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.n_tiles = static_cast<int32_t*>(take(mfma ? 2 * sizeof(int32_t) : 0));
     w.h16 = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * P * L.inter : 0));
     w.h_sh16 = static_cast<uint16_t*>(take(mfma && shared ? sizeof(uint16_t) * T * L.shared_inter : 0));
+    w.xn = static_cast<float*>(take((L.flags & WL_MOE_PRE_NORM) ? sizeof(float) * T * L.hidden : 0));
     w.bytes = off;
     return w;
 }
@@ -971,6 +993,8 @@ int check_layer(const WlMoeLayer* L) {
 
 static int check_one_layer(const WlMoeLayer* L) {
     if (!L) return WL_EINVAL_NULL;
+    if ((L->flags & WL_MOE_PRE_NORM) && (!(L->norm_eps >= 0.0f) || reinterpret_cast<uintptr_t>(L->norm_weight) % 16))
+        return WL_EINVAL_SHAPE;
     if (!L->gate_up || !L->down || !L->router) return WL_EINVAL_NULL;
     if (block_bytes(L->gate_up_type) < 0 || block_bytes(L->down_type) < 0) return WL_EINVAL_TYPE;
     if (L->hidden <= 0 || L->hidden % kQK != 0 || L->hidden > kRouterSeg * 32 * kRouterMaxJ) return WL_EINVAL_SHAPE;
@@ -1186,6 +1210,7 @@ const char* wl_error_string(int code) {
         case WL_EINVAL_WORKSPACE: return "workspace is NULL or smaller than wl_moe_workspace_bytes()";
         case WL_EINVAL_DTYPE: return "output dtype must be WL_DTYPE_F32 or WL_DTYPE_BF16";
         case WL_EINVAL_COUNT: return "expert count must be in 1..64";
+        case WL_EINVAL_OVERLAP: return "y overlaps x: the layer writes y while x is still being read";
         case WL_ESYNC:
             return "a fused-kernel workgroup gave up waiting for another (not every workgroup was resident): the "
                    "outputs of the calls since the last status query hold NaN";
@@ -1230,6 +1255,11 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     if (!x || !y) return WL_EINVAL_NULL;
     if (tokens <= 0 || tokens > kMaxTokens) return WL_EINVAL_SHAPE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16) return WL_EINVAL_ALIGN;
+    {  // y and x must not overlap: the fused kernel reads x in every workgroup while the owners write y
+        const uintptr_t xb = reinterpret_cast<uintptr_t>(x), yb = reinterpret_cast<uintptr_t>(y);
+        const uintptr_t n = static_cast<uintptr_t>(tokens) * static_cast<uintptr_t>(layer->hidden) * sizeof(float);
+        if (xb < yb + n && yb < xb + n) return WL_EINVAL_OVERLAP;
+    }
     const WlMoeLayer& L = *layer;
     const Workspace need = carve(L, tokens, nullptr);
     if (!workspace || workspace_bytes < need.bytes) return WL_EINVAL_WORKSPACE;
@@ -1253,6 +1283,12 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     // stage boundaries for wl_moe_layer_profile: event i is recorded before stage i, event kMoeStages after the last
     auto mark = record;
     mark(0);
+    const float* resid = (L.flags & WL_MOE_RESIDUAL) ? x : nullptr;
+    if (L.flags & WL_MOE_PRE_NORM) {  // every stage below runs on the normalized input
+        k_rms_norm<<<static_cast<unsigned>((tokens + 3) / 4), 256, 0, s>>>(x, L.norm_weight, L.norm_eps,
+                                                                           static_cast<int>(tokens), L.hidden, w.xn);
+        x = w.xn;
+    }
     // an MFMA plan: the router also writes x as bf16 and the sort also writes the GEMM tile lists
     const ExpertPlan plan = expert_plan(L, tokens);
     const bool mfma = plan != kPlanGemv;
@@ -1292,10 +1328,11 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     if (mfma)
         k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
                                                   w.wts, w.o,
-                                                  shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg, y);
+                                                  shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg,
+                                                  resid, y);
     else
         k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, y);
+                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y);
     rc = launch_status();
     mark(6);
     return rc;

@@ -11,8 +11,48 @@ namespace wl {
 // on the other half's row; each lane owns the 64-value segments s = slot, slot + 32, ... and chains fused
 // multiply-adds over them in ascending k; the segment partials are then added left to right. Every lane of a
 // half returns its row's sum (no bias). Call with the whole wavefront; `valid` may differ between the halves.
+// x as stored, or scaled on load (RMSNorm): x4(i) returns the float4 of values 4 i .. 4 i + 3.
+struct PlainX {
+    const float* x;
+    __device__ __forceinline__ float4 operator()(int i) const { return reinterpret_cast<const float4*>(x)[i]; }
+};
+
+// The RMSNorm of engines/base.py:27-31 (zero-centered: x * inv * (1 + w)) applied as x is loaded, in the fixed
+// order the layer documents: inv from norm_inv, then each value rounded after each product. w may be NULL (0).
+struct NormX {
+    const float* x;
+    const float* w;
+    float inv;
+    __device__ __forceinline__ float4 operator()(int i) const {
+        const float4 v = reinterpret_cast<const float4*>(x)[i];
+        float4 g = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (w) {
+            const float4 u = reinterpret_cast<const float4*>(w)[i];
+            g = make_float4(__fadd_rn(1.f, u.x), __fadd_rn(1.f, u.y), __fadd_rn(1.f, u.z), __fadd_rn(1.f, u.w));
+        }
+        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                           __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+    }
+};
+
+template <typename XF>
+__device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ wr, bool valid, int H, int lane);
+
 __device__ __forceinline__ float router_row(const float* __restrict__ x, const float* __restrict__ wr, bool valid,
                                             int H, int lane) {
+    return router_row_x(PlainX{x}, wr, valid, H, lane);
+}
+
+// 1 / sqrt(s / H + eps), each step correctly rounded once (the norm's scale from the sum of squares s). The square
+// root is __builtin_sqrtf (llvm.sqrt.f32, expanded to a correctly rounded sequence since HIP builds keep fp32
+// division and square root correctly rounded by default); HIP's __fsqrt_rn maps to the native v_sqrt_f32, which is
+// not, and differs from a correctly rounded root in the last bit for about a third of inputs.
+__device__ __forceinline__ float norm_inv(float s, int H, float eps) {
+    return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s, static_cast<float>(H)), eps)));
+}
+
+template <typename XF>
+__device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ wr, bool valid, int H, int lane) {
     const int slot = lane & 31, src_base = lane & 32;
     const int nseg = H / kRouterSeg;
     float total = 0.0f;
@@ -23,10 +63,9 @@ __device__ __forceinline__ float router_row(const float* __restrict__ x, const f
         const int s = slot + 32 * j;
         if (valid && s < nseg) {
             const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
-            const float4* xp = reinterpret_cast<const float4*>(x + s * kRouterSeg);
 #pragma unroll
             for (int i = 0; i < kRouterSeg / 4; i++) {
-                const float4 wv = wp[i], xv = xp[i];
+                const float4 wv = wp[i], xv = x4(s * (kRouterSeg / 4) + i);
                 p = __builtin_fmaf(xv.x, wv.x, p);
                 p = __builtin_fmaf(xv.y, wv.y, p);
                 p = __builtin_fmaf(xv.z, wv.z, p);

@@ -75,6 +75,9 @@ struct FusedArgs {
     const float* next_sh_gate;
     const uint8_t* next_sh_gate_up;
     const uint8_t* next_sh_down;
+    const float* norm_w;  // NORM: the RMSNorm weight (zero-centered) or NULL
+    float norm_eps;
+    int residual;         // y = x + MoE
 };
 
 // The 128-byte lines of what wavefront slot t reads in phase A (router row t, or the shared expert's gate row j and
@@ -161,7 +164,7 @@ __device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_
     }
 }
 
-template <int GU, int DN, int EJ, int NBD>
+template <int GU, int DN, int EJ, int NBD, bool NORM>
 __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     constexpr int WIDTH = 8 * NBD;  // lanes per down row (8 per block)
     constexpr int R = 64 / WIDTH;   // down rows per wavefront pass
@@ -194,6 +197,18 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     bool ok = true;
     const bool publish = b != a.silent_wg;
 
+    // The layer's input: x, or with NORM its RMSNorm, applied as each value is loaded. Every wavefront takes the
+    // sum of squares itself (router_row of x with itself: the router's order), so no barrier is needed.
+    float inv = 1.0f;
+    if constexpr (NORM) inv = norm_inv(router_row(a.x, a.x, true, H, lane), H, a.norm_eps);
+    const NormX norm_x{a.x, a.norm_w, inv};
+    auto xload = [&](int i) -> float4 {
+        if constexpr (NORM)
+            return norm_x(i);
+        else
+            return reinterpret_cast<const float4*>(a.x)[i];
+    };
+
     // x, for the gate_up dot products: a lane's two 16-value runs of its block gi
     const int nb = H / kQK;  // <= 8: one gate/up block per lane group
     const bool gu_lane = gi < nb;
@@ -201,8 +216,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     const int64_t gu_rs = static_cast<int64_t>(nb) * BlockInfo<GU>::bytes;
     float4 xl[4], xh[4];  // loaded now; their sums are taken where they are used, so nothing waits for x here
     if (gu_lane) {
-        load_run(a.x + lo_gu, xl);
-        load_run(a.x + hi_gu, xh);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xl[i] = xload(lo_gu / 4 + i);
+            xh[i] = xload(hi_gu / 4 + i);
+        }
     }
     auto gate_up_dots = [&](const Lane32& lg, const Lane32& lu, float& g, float& u) {
         float ag = 0.0f, au = 0.0f;
@@ -229,7 +247,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const int row = t;
             const bool valid = lane < 32;
             const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
-            const float total = router_row(a.x, wr, valid, H, lane);
+            const float total = router_row_x(xload, wr, valid, H, lane);
             if ((lane & 31) == 0 && valid && publish)
                 put_tagged(a.sync, kTagLogits + 2 * row, tag,
                            (row < E && a.router_bias) ? __fadd_rn(total, a.router_bias[row]) : total);
@@ -483,6 +501,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         for (int s = 0; s < k; s++)
             acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
         if (shared) acc = acc + sgv * lds_sh[r];
+        if (a.residual) acc = __fadd_rn(a.x[kOwnRows * b + r], acc);
         a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
     }
     if (!all_ok && threadIdx.x == 0)  // a vector atomic, visible to the host's status query
@@ -503,22 +522,29 @@ __global__ void k_zero_words(uint32_t* p, int n) {
 static const void* fused_instance(const WlMoeLayer& L) {
     const int ej = L.n_experts <= 64 ? 1 : L.n_experts <= 128 ? 2 : 4;
     const int nbd = L.inter / kQK;
-#define WL_FUSED_PICK(DN)                                                                                          \
+    const bool norm = (L.flags & WL_MOE_PRE_NORM) != 0;
+#define WL_FUSED_PICK(DN, NORM)                                                                                    \
     switch (ej * 8 + (nbd == 1 ? 1 : nbd == 2 ? 2 : 4)) {                                                           \
-        case 9: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 1>);                       \
-        case 10: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 2>);                      \
-        case 12: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 4>);                      \
-        case 17: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 1>);                      \
-        case 18: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 2>);                      \
-        case 20: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 4>);                      \
-        case 33: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 1>);                      \
-        case 34: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 2>);                      \
-        default: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 4>);                     \
+        case 9: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 1, NORM>);                 \
+        case 10: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 2, NORM>);                \
+        case 12: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 4, NORM>);                \
+        case 17: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 1, NORM>);                \
+        case 18: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 2, NORM>);                \
+        case 20: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 4, NORM>);                \
+        case 33: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 1, NORM>);                \
+        case 34: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 2, NORM>);                \
+        default: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 4, NORM>);               \
     }
     if (L.down_type == WL_TYPE_Q4_K) {
-        WL_FUSED_PICK(WL_TYPE_Q4_K)
+        if (norm) {
+            WL_FUSED_PICK(WL_TYPE_Q4_K, true)
+        }
+        WL_FUSED_PICK(WL_TYPE_Q4_K, false)
     }
-    WL_FUSED_PICK(WL_TYPE_Q6_K)
+    if (norm) {
+        WL_FUSED_PICK(WL_TYPE_Q6_K, true)
+    }
+    WL_FUSED_PICK(WL_TYPE_Q6_K, false)
 #undef WL_FUSED_PICK
 }
 
@@ -594,6 +620,9 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
     const bool starve = (L.flags & WL_MOE_TEST_STARVE) != 0;
     a.spin_limit = starve ? kStarveSpinLimit : kSpinLimit;
     a.silent_wg = starve ? a.G - 1 : -1;
+    a.norm_w = L.norm_weight;
+    a.norm_eps = L.norm_eps;
+    a.residual = (L.flags & WL_MOE_RESIDUAL) ? 1 : 0;
     const WlMoeLayer* nx = L.next;
     // the next layer's phase A maps tasks to workgroups and wavefronts the same way only with the same shapes
     if (nx && nx->hidden == L.hidden && nx->n_experts == L.n_experts && nx->inter == L.inter &&

@@ -20,7 +20,7 @@ BLOCK_SIZES = {"Q4_K": (256, 144), "Q6_K": (256, 210)}  # gguf/reader.py:25,27
 MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many tokens (gguf/metal.py:20)
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
-MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA, MOE_TEST_STARVE = 1, 2, 4, 8
+MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA, MOE_TEST_STARVE, MOE_PRE_NORM, MOE_RESIDUAL = 1, 2, 4, 8, 16, 32
 ESYNC = -10  # wl_moe_workspace_status: a fused-kernel wait gave up
 NOALLOC_SCRATCH_BYTES = 16 << 20  # WL_NOALLOC_SCRATCH_BYTES
 
@@ -45,7 +45,8 @@ class WlMoeLayer(ctypes.Structure):
         ("shared_down_type", ctypes.c_int32), ("hidden", ctypes.c_int32), ("inter", ctypes.c_int32),
         ("shared_inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("top_k", ctypes.c_int32),
         ("norm_topk_prob", ctypes.c_int32), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32),
-        ("next", ctypes.c_void_p),
+        ("next", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p), ("norm_eps", ctypes.c_float),
+        ("reserved2", ctypes.c_int32),
     ]
 
 

@@ -6,7 +6,8 @@ import ctypes
 
 import torch
 
-from . import (MOE_FORCE_MFMA, MOE_NO_FUSED, MOE_NO_MFMA, TYPE_IDS, WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
+from . import (MOE_FORCE_MFMA, MOE_NO_FUSED, MOE_NO_MFMA, MOE_PRE_NORM, MOE_RESIDUAL, TYPE_IDS, WlMoeLayer, _on_gpu,
+               _stream, _type_id, check, library, row_bytes)
 
 
 def _ptr(t):
@@ -20,12 +21,16 @@ class MoELayer:
              (gate rows first, gguf/compiler.py:69-88); down: uint8 [n_experts, hidden * row_bytes(down_type,
              inter)]; router: fp32 [n_experts, hidden]; router_bias: fp32 [n_experts] or None; shared_gate_up,
              shared_down: the shared expert's matrices (or None); shared_gate: fp32 [hidden] or None.
-    Tensors may be views into a larger store; each expert's bytes must be contiguous (a row of a 2-D tensor)."""
+    Tensors may be views into a larger store; each expert's bytes must be contiguous (a row of a 2-D tensor).
+    pre_norm: run on the zero-centered RMSNorm of x (norm_weight fp32 [hidden] or None for 0, norm_eps), as the
+    model calls the layer on rms_norm(x) (engines/qwen36/model.py:22, engines/base.py:27-31); residual: return
+    x + MoE(...), the residual add of the same line."""
 
     def __init__(self, *, gate_up, down, router, hidden: int, inter: int, n_experts: int, top_k: int,
                  norm_topk_prob: bool = True, gate_up_type: str = "Q4_K", down_type: str = "Q6_K",
                  router_bias=None, shared_gate_up=None, shared_down=None, shared_gate=None, shared_inter=None,
-                 shared_gate_up_type=None, shared_down_type=None, fused: bool = True, mfma: str = "auto"):
+                 shared_gate_up_type=None, shared_down_type=None, fused: bool = True, mfma: str = "auto",
+                 pre_norm: bool = False, norm_weight=None, norm_eps: float = 1e-6, residual: bool = False):
         for name, t in (("gate_up", gate_up), ("down", down), ("router", router)):
             _on_gpu(t, name)
         if router.dtype != torch.float32:
@@ -64,12 +69,22 @@ class MoELayer:
         if mfma not in ("auto", "never", "always"):
             raise ValueError("mfma must be 'auto', 'never' or 'always'")
         s.flags = (0 if fused else MOE_NO_FUSED) | {"auto": 0, "never": MOE_NO_MFMA, "always": MOE_FORCE_MFMA}[mfma]
+        self.norm_weight = None
+        if pre_norm:
+            s.flags |= MOE_PRE_NORM
+            if norm_weight is not None:
+                self.norm_weight = torch.as_tensor(norm_weight).to(device=self.device, dtype=torch.float32).reshape(-1).contiguous()
+            s.norm_weight = _ptr(self.norm_weight)
+            s.norm_eps = float(norm_eps)
+        if residual:
+            s.flags |= MOE_RESIDUAL
         self.struct = s
         check(library().wl_moe_check(ctypes.byref(s)))
 
     @classmethod
-    def from_host(cls, lw: dict, device="cuda", fused: bool = True, mfma: str = "auto"):
-        """From a layer dict of numpy arrays (gguf.synth.moe_layer's layout), copied to the GPU."""
+    def from_host(cls, lw: dict, device="cuda", fused: bool = True, mfma: str = "auto", **kw):
+        """From a layer dict of numpy arrays (gguf.synth.moe_layer's layout), copied to the GPU; kw: pre_norm,
+        norm_weight, norm_eps, residual."""
         def dev(a):
             return None if a is None else torch.from_numpy(a).to(device)
         return cls(gate_up=dev(lw["gate_up"].reshape(lw["experts"], -1)),
@@ -80,7 +95,7 @@ class MoELayer:
                    shared_gate_up=dev(lw.get("shared_gate_up")), shared_down=dev(lw.get("shared_down")),
                    shared_gate=dev(lw.get("shared_gate")), shared_inter=lw.get("shared_inter"),
                    shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"),
-                   fused=fused, mfma=mfma)
+                   fused=fused, mfma=mfma, **kw)
 
     def set_next(self, layer: "MoELayer" = None):
         """The layer the caller runs after this one (or None). With the same shapes, a batch-1 call pulls the rows
