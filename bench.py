@@ -229,6 +229,167 @@ def profile_stages(torch, hip, layers, xs, T, ws, reps=2):
     return {n: sum(v) / len(v) for n, v in per.items()}
 
 
+def rms_norm_torch(torch, x, w, eps=1e-6):
+    """engines/base.py:27-31, zero-centered (x * rsqrt(mean(x^2) + eps) * (1 + w)), in torch fp32: the input of
+    the next-layer guess (it only feeds a routing guess, so torch's own rounding is fine here)."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w)
+
+
+def run_chained(torch, hip, layers, steps, warmup, n_sets):
+    """Decode b=1 with each layer's input the previous layer's output, as the model chains them:
+    x_{l+1} = x_l + MoE_l(rms_norm_l(x_l)) (engines/qwen36/model.py:22; the attention half is not part of this
+    path). One launch per layer (the layer's pre-norm and residual flags), the stack captured as one graph per
+    starting vector and replayed; the graph's output is checked bit for bit against an eager pass. Also measures
+    how often the reference's next-layer guess, layer l+1's router on rms_norm_{l+1}(x_l) before layer l's experts
+    are added (engines/base.py:392-406, engines/qwen36/model.py:30-31), names layer l+1's actual experts."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4242)
+    L = len(layers)
+    norm_w = [torch.randn(HIDDEN, device="cuda", generator=gen) * 0.1 for _ in range(L)]
+    chain = [layer.with_norm(norm_w[l]) for l, layer in enumerate(layers)]
+    for l in range(L):
+        chain[l].set_next(chain[(l + 1) % L])
+    x0 = [torch.randn(1, HIDDEN, device="cuda", generator=gen) for _ in range(n_sets)]
+    xs = torch.empty(L, 1, HIDDEN, device="cuda")  # layer l writes x_{l+1} into xs[l]
+    ws = new_workspace(max(layer.workspace_bytes(1) for layer in chain), "cuda")
+
+    def stack(x, ids=None):
+        for l, layer in enumerate(chain):
+            layer(x if l == 0 else xs[l - 1], out=xs[l], workspace=ws, ids=None if ids is None else ids[l])
+
+    ids = torch.empty(n_sets, L, 1, TOP_K, dtype=torch.int32, device="cuda")
+    hits = []
+    eager_out = []
+    for s in range(n_sets):  # eager passes: routing of every layer, and each step's last output
+        stack(x0[s], ids[s])
+        for l in range(L - 1):
+            x_l = x0[s] if l == 0 else xs[l - 1]
+            _, guess, _ = layers[l + 1].route(rms_norm_torch(torch, x_l, norm_w[l + 1]))
+            hits.append(torch.isin(guess[0], ids[s, l + 1, 0]).sum())
+        eager_out.append(xs[L - 1].clone())
+    torch.cuda.synchronize()
+    hit_rate = float(torch.stack(hits).sum()) / (len(hits) * TOP_K)
+    graphs = []
+    capture = torch.cuda.Stream()
+    for s in range(n_sets):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=capture):
+            stack(x0[s])
+        graphs.append(g)
+    for s in range(n_sets):
+        graphs[s].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(xs[L - 1], eager_out[s]), "chained decode: graph replay differs from the eager pass"
+    for i in range(warmup):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % n_sets].replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    assert torch.isfinite(xs).all(), "chained decode: non-finite outputs"
+    for layer in chain:
+        layer.set_next(None)
+    us_layer = ms * 1000.0 / (steps * L)
+    bytes_layer = layer_bytes(1, TOP_K)
+    log(f"decode b=1 chained: {ms / steps:.3f} ms/step, {us_layer:.2f} us/layer, "
+        f"{bytes_layer / us_layer / 1e3:.0f} GB/s, next-layer guess hit rate {hit_rate:.3f}")
+    del graphs
+    return {"us_per_token_layer": round(us_layer, 3), "ms_per_step": round(ms / steps, 4),
+            "hbm_gbps": round(bytes_layer / us_layer / 1e3, 1), "steps": steps, "starting_vectors": n_sets,
+            "graph_matches_eager": True, "next_layer_guess_hit_rate": round(hit_rate, 4),
+            "guess": "top-8 of layer l+1's router on rms_norm_{l+1}(x_l), scored against layer l+1's experts",
+            "norm": "zero-centered RMSNorm, weights N(0, 0.1), eps 1e-6"}
+
+
+def routing_margins(torch, logits):
+    """Per-token gap between the 8th and 9th largest router logits over the [N, E] logits of a workload, and the
+    tokens whose 8th and 9th fp32 softmax probabilities are equal: the reference selects on probabilities
+    (engines/base.py:93-94), where exp rounding can tie distinct logits that the logit-based selection orders."""
+    top = torch.topk(logits, TOP_K + 1, dim=-1).values
+    m = (top[:, TOP_K - 1] - top[:, TOP_K]).float()
+    probs = torch.topk(torch.softmax(logits, dim=-1), TOP_K + 1, dim=-1).values
+    return {"tokens": int(m.numel()), "min": float(m.min()), "p1": float(torch.quantile(m, 0.01)),
+            "median": float(m.median()), "logit_ties": int((m == 0).sum()),
+            "prob_ties": int((probs[:, TOP_K - 1] == probs[:, TOP_K]).sum())}
+
+
+def layer_logits(torch, layers, inputs):
+    """Router logits of layers[l] on inputs[l] for every l, concatenated."""
+    out = [layer.route(x, return_logits=True)[3] for layer, x in zip(layers, inputs)]
+    return torch.cat(out)
+
+
+def run_small_configs(torch, hip, reps=5):
+    """The single-matrix and single-expert workloads on the GPU, each call on its own copy of the weights so the
+    256 MB MALL cannot serve repeats: 1024 copies of the 512 x 2048 Q4_K matrix (604 MB) through wl_gemv, and 256
+    copies of one expert (gate/up Q4_K 512 x 2048, down Q6_K 2048 x 512; 522 MB) through wl_moe_layer as a
+    one-expert, top-1 layer without a shared expert (its router is a 2048-value dot product and its routing
+    weight 1). All calls of a workload are captured in one graph, replayed `reps` times; figures are per call."""
+    lib = hip.library()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+
+    def timed(fn, calls):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1000.0 / (reps * calls)
+
+    n0, rows, k = 1024, 512, 2048
+    w0 = gen_q4k(torch, n0 * rows * (k // 256), gen).view(n0, -1)
+    x0 = torch.randn(1, k, device="cuda", generator=gen)
+    y0 = torch.empty(n0, rows, device="cuda")
+
+    def gemvs():
+        stream = torch.cuda.current_stream().cuda_stream
+        for i in range(n0):
+            hip.check(lib.wl_gemv(12, w0[i].data_ptr(), rows, k, Q4K_ROW, x0.data_ptr(), 1, y0[i].data_ptr(),
+                                  stream))
+
+    us0 = timed(gemvs, n0)
+    c0_bytes = 600064
+    del w0
+    n1 = 256
+    gate_up = gen_q4k(torch, n1 * 2 * INTER * (HIDDEN // 256), gen).view(n1, -1)
+    down = gen_q6k(torch, n1 * HIDDEN * (INTER // 256), gen).view(n1, -1)
+    router = torch.randn(1, HIDDEN, device="cuda", generator=gen) * 0.02
+    experts = [hip.MoELayer(gate_up=gate_up[i:i + 1], down=down[i:i + 1], router=router, hidden=HIDDEN,
+                            inter=INTER, n_experts=1, top_k=1) for i in range(n1)]
+    x1 = torch.randn(1, HIDDEN, device="cuda", generator=gen)
+    y1 = torch.empty(n1, 1, HIDDEN, device="cuda")
+    ws = new_workspace(experts[0].workspace_bytes(1), "cuda")
+
+    def expert_calls():
+        for i, e in enumerate(experts):
+            e(x1, out=y1[i], workspace=ws)
+
+    us1 = timed(expert_calls, n1)
+    c1_bytes = 2056192
+    assert torch.isfinite(y0).all() and torch.isfinite(y1).all()
+    log(f"config 0 (Q4_K GEMV 512x2048): {us0:.2f} us/call, {c0_bytes / us0 / 1e3:.0f} GB/s; config 1 (one "
+        f"expert, b=1, {experts[0].plan(1)}): {us1:.2f} us/call, {c1_bytes / us1 / 1e3:.0f} GB/s")
+    return {"config0_gemv": {"us_per_call": round(us0, 3), "bytes": c0_bytes, "gbps": round(c0_bytes / us0 / 1e3, 1),
+                             "weight_copies": n0, "rotated_mb": round(n0 * rows * Q4K_ROW / 1e6, 1)},
+            "config1_expert": {"us_per_call": round(us1, 3), "bytes": c1_bytes,
+                               "gbps": round(c1_bytes / us1 / 1e3, 1), "weight_copies": n1,
+                               "rotated_mb": round(n1 * EXPERT_BYTES / 1e6, 1), "plan": experts[0].plan(1)},
+            "graph": f"all calls of a workload in one graph, {reps} replays"}
+
+
 def measured_traffic(kernel):
     """HBM bytes per dispatch of `kernel` from the committed counter summary (rocprofv3 FETCH_SIZE and WRITE_SIZE
     runs of this script, each scaled by the same counter's reading for a plain copy of known size), or None."""
@@ -241,27 +402,97 @@ def measured_traffic(kernel):
     return None
 
 
-def cpu_baseline(budget_s=12.0):
-    """The CPU oracle (numpy dequantize of the touched experts + fp32 BLAS matmuls): decode of single tokens
-    through one full-shape layer, until the time budget is spent."""
+def cpu_info():
+    """The host's CPU model (lscpu, else /proc/cpuinfo) and counts."""
+    import subprocess
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if model is None and os.path.exists("/proc/cpuinfo"):
+        model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), None)
+    return {"model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline():
+    """The CPU oracle (numpy dequantize of the touched weights, then fp32 BLAS matmuls, fp32 router and combine;
+    the reference's CPU path gguf/quants.py + matmul restated) on this host, for each workload:
+      config 0: the 512 x 2048 Q4_K GEMV (seed 0), repeated for >= 0.5 s;
+      config 1: one expert at batch 1 (seed 0), repeated for >= 0.5 s;
+      config 2: the full layer (seed 1) at batch 1, >= 8 tokens over >= 3 s, each a new token;
+      config 3: 64 tokens through 40 layer passes with Zipf(1.1) routing; the passes share the seed-1 expert
+                weights (the oracle dequantizes from the quantized bytes on every pass, so sharing saves no work)
+                and each draws its own Zipf permutation and tokens;
+      config 4: one layer x 4096 tokens, timed once, extrapolated x40 to the 40-layer chunk.
+    Threads: the BLAS pool and torch use the host's CPU share (OMP_NUM_THREADS when set, as on machines that
+    allot a share of their cores to each GPU, else os.cpu_count())."""
     import numpy as np
-    from threadpoolctl import threadpool_info
+    import torch
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from gguf import synth
     from oracle import moe_ref
-    lw = synth.moe_layer(1)
-    tokens = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        moe_ref.layer(synth.tokens(10 + tokens, 1), lw)
-        tokens += 1
-    dt = time.perf_counter() - t0
-    threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
-    us = dt / tokens * 1e6
-    return {"value": round(us, 1), "unit": "us/token/layer", "cores": int(threads), "kind": "port",
-            "sample": f"{tokens} decode tokens (b=1) through one full-shape layer (256 experts, top-8, shared; "
-                      f"seed-1 weights), numpy dequantize + fp32 BLAS matmul; {np.__name__} {np.__version__}",
-            "hbm_equiv_gbps": round(layer_bytes(1, 8) / us / 1e3, 2)}
+    from oracle.quants_ref import dequantize_matrix
+    n_threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count())
+    torch.set_num_threads(n_threads)
+    out = {}
+    with threadpool_limits(limits=n_threads, user_api="blas"):
+        blas = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+
+        def repeat(fn, min_s, min_n=3):  # one untimed call first (page faults, pool start-up)
+            fn(-1)
+            n, t0 = 0, time.perf_counter()
+            while n < min_n or time.perf_counter() - t0 < min_s:
+                fn(n)
+                n += 1
+            return (time.perf_counter() - t0) / n, n
+
+        c0 = synth.gemv_case(0)
+        dt, n = repeat(lambda i: c0["x"] @ dequantize_matrix(c0["w"], "Q4_K", 512, 2048).T, 0.5)
+        out["config0_gemv"] = {"us_per_call": round(dt * 1e6, 1), "calls": n, "gbps": round(600064 / dt / 1e9, 3)}
+        c1 = synth.expert_case(0)
+
+        def expert(i):
+            gu = np.concatenate((dequantize_matrix(c1["gate"], "Q4_K", 512, 2048),
+                                 dequantize_matrix(c1["up"], "Q4_K", 512, 2048)))
+            moe_ref.expert_ffn(c1["x"], gu, dequantize_matrix(c1["down"], "Q6_K", 2048, 512), 512)
+        dt, n = repeat(expert, 0.5)
+        out["config1_expert"] = {"us_per_call": round(dt * 1e6, 1), "calls": n,
+                                 "gbps": round(2056192 / dt / 1e9, 3)}
+        lw = synth.moe_layer(1)
+        dt, n = repeat(lambda i: moe_ref.layer(synth.tokens(11 + i, 1), lw), 3.0, 8)
+        out["config2_decode_b1"] = {"us_per_token_layer": round(dt * 1e6, 1), "tokens": n,
+                                    "gbps": round(layer_bytes(1, TOP_K) / dt / 1e9, 3)}
+        rng = np.random.default_rng(3)
+        t3, unique = 0.0, []
+        for p in range(LAYERS):
+            lz = dict(lw, router_bias=synth.zipf_bias(rng, EXPERTS, 1.1))
+            x = synth.tokens(100 + p, 64)
+            t0 = time.perf_counter()
+            _, ids, _, _ = moe_ref.layer(x, lz, return_routing=True)
+            t3 += time.perf_counter() - t0
+            unique.append(len(np.unique(ids)))
+        out["config3_decode_b64"] = {"us_per_token_layer": round(t3 / (LAYERS * 64) * 1e6, 1),
+                                     "ms_per_step": round(t3 * 1e3, 1), "layers": LAYERS,
+                                     "mean_unique_experts": round(float(np.mean(unique)), 1)}
+        x = synth.tokens(7, 4096)
+        t0 = time.perf_counter()
+        moe_ref.layer(x, lw)
+        t4 = time.perf_counter() - t0
+        out["config4_prefill_4096"] = {"ms_per_layer": round(t4 * 1e3, 1),
+                                       "ms_per_chunk_extrapolated_x40": round(t4 * 1e3 * LAYERS, 1),
+                                       "tok_per_s": round(4096 / (t4 * LAYERS), 2), "timed_layers": 1}
+    us = out["config2_decode_b1"]["us_per_token_layer"]
+    return {"value": us, "unit": "us/token/layer", "cores": n_threads, "kind": "port",
+            "sample": f"config 2 line: {out['config2_decode_b1']['tokens']} decode tokens (b=1) through one "
+                      "full-shape layer (256 experts, top-8, shared; seed-1 weights), numpy dequantize + fp32 BLAS "
+                      "matmul; per-config figures in configs",
+            "hbm_equiv_gbps": round(layer_bytes(1, TOP_K) / us / 1e3, 3),
+            "threads": {"torch_get_num_threads": torch.get_num_threads(), "blas_threads": int(blas),
+                        "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")},
+            "cpu": cpu_info(), "configs": out}
 
 
 def main():
@@ -276,6 +507,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-load", action="store_true")
     ap.add_argument("--skip-linear", action="store_true")
+    ap.add_argument("--skip-chained", action="store_true")
+    ap.add_argument("--skip-small", action="store_true", help="skip the GPU timings of configs 0 and 1")
     ap.add_argument("--load-layers", type=int, default=8,
                     help="full-shape layers in the synthetic GGUF file of the loader measurement")
     ap.add_argument("--no-next", action="store_true",
@@ -348,9 +581,15 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(dominant), "algorithmic_bytes": int(dom_bytes)},
     }
+    margins = {"config2_decode_b1": routing_margins(
+        torch, torch.cat([layer_logits(torch, layers, xset) for xset in d1["xs"]]))}
     del d1
+    if not args.skip_chained:
+        result["decode_b1_chained"] = run_chained(torch, hip, layers, args.steps, args.warmup, args.sets)
     if not args.skip_prefill:
-        result["prefill"] = run_prefill(torch, hip, layers, 4096, steps=2)
+        result["prefill"], x_prefill = run_prefill(torch, hip, layers, 4096, steps=2)
+        margins["config4_prefill_4096"] = routing_margins(torch, layer_logits(torch, layers, [x_prefill] * len(layers)))
+        del x_prefill
     if not args.skip_b64:
         del layers
         torch.cuda.empty_cache()
@@ -361,8 +600,14 @@ def main():
                                 "us_per_layer": round(d64["us_per_layer"], 2),
                                 "hbm_gbps": round(d64["hbm_gbps"], 1),
                                 "mean_unique_experts": round(sum(d64["unique"]) / len(d64["unique"]), 1),
-                                "routing": "Zipf(1.1) router bias"}
-        del d64
+                                "routing": "Zipf(1.1) router bias", "plan": zl[0].plan(64)}
+        margins["config3_decode_b64"] = routing_margins(
+            torch, torch.cat([layer_logits(torch, zl, xset) for xset in d64["xs"]]))
+        del d64, zl
+        torch.cuda.empty_cache()
+    result["routing_margins"] = margins
+    if not args.skip_small:
+        result["small_configs_gpu"] = run_small_configs(torch, hip)
     if not args.skip_load:
         result["gguf_load"] = run_gguf_load(torch, args.load_layers)
     if not args.skip_linear:
@@ -394,7 +639,7 @@ def run_prefill(torch, hip, layers, T, steps):
     return {"tokens": T, "ms_per_chunk": round(ms, 2), "tok_per_s": round(T / ms * 1e3, 1),
             "tflops": round(flops / ms / 1e9, 2), "mfma_frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
             "path": layers[0].plan(T) + ": tiled fp32 router, bf16 MFMA grouped expert GEMMs (in-register "
-                    "Q4_K/Q6_K dequant), fp32 combine"}
+                    "Q4_K/Q6_K dequant), fp32 combine"}, x
 
 
 def run_linear(torch, hip, rows=2048, k=2048, T=4096, reps=20):

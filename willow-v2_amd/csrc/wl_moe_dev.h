@@ -19,19 +19,21 @@ struct PlainX {
 
 // The RMSNorm of engines/base.py:27-31 (zero-centered: x * inv * (1 + w)) applied as x is loaded, in the fixed
 // order the layer documents: inv from norm_inv, then each value rounded after each product. w may be NULL (0).
+__device__ __forceinline__ float4 norm_apply(float4 v, bool has_w, float4 u, float inv) {
+    float4 g = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (has_w) g = make_float4(__fadd_rn(1.f, u.x), __fadd_rn(1.f, u.y), __fadd_rn(1.f, u.z), __fadd_rn(1.f, u.w));
+    return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                       __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+}
+
 struct NormX {
     const float* x;
     const float* w;
     float inv;
     __device__ __forceinline__ float4 operator()(int i) const {
         const float4 v = reinterpret_cast<const float4*>(x)[i];
-        float4 g = make_float4(1.f, 1.f, 1.f, 1.f);
-        if (w) {
-            const float4 u = reinterpret_cast<const float4*>(w)[i];
-            g = make_float4(__fadd_rn(1.f, u.x), __fadd_rn(1.f, u.y), __fadd_rn(1.f, u.z), __fadd_rn(1.f, u.w));
-        }
-        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x), __fmul_rn(__fmul_rn(v.y, inv), g.y),
-                           __fmul_rn(__fmul_rn(v.z, inv), g.z), __fmul_rn(__fmul_rn(v.w, inv), g.w));
+        const float4 u = w ? reinterpret_cast<const float4*>(w)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        return norm_apply(v, w != nullptr, u, inv);
     }
 };
 

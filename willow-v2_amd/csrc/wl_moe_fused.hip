@@ -73,6 +73,7 @@ struct FusedArgs {
     // the next layer's rows read before its routing is known (NULL next_router: no prefetch); same shapes
     const float* next_router;
     const float* next_sh_gate;
+    const float* next_norm_w;  // the next layer's RMSNorm weight, when it has one
     const uint8_t* next_sh_gate_up;
     const uint8_t* next_sh_down;
     const float* norm_w;  // NORM: the RMSNorm weight (zero-centered) or NULL
@@ -177,6 +178,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
+    __shared__ __attribute__((aligned(16))) float lds_xn[NORM ? kFusedMaxHidden : 4];  // NORM: the normalized x
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int b = blockIdx.x, G = a.G;
     const int H = a.H, I = a.I, E = a.E, k = a.k;
@@ -197,14 +199,33 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     bool ok = true;
     const bool publish = b != a.silent_wg;
 
-    // The layer's input: x, or with NORM its RMSNorm, applied as each value is loaded. Every wavefront takes the
-    // sum of squares itself (router_row of x with itself: the router's order), so no barrier is needed.
-    float inv = 1.0f;
-    if constexpr (NORM) inv = norm_inv(router_row(a.x, a.x, true, H, lane), H, a.norm_eps);
-    const NormX norm_x{a.x, a.norm_w, inv};
+    // The layer's input: x, or with NORM its RMSNorm, written once to LDS by the workgroup. Thread i loads x's
+    // values 4i..4i+3 (and the norm weight's), so x crosses from L2 once per workgroup; wavefront 0 takes the sum of
+    // squares from LDS in the router's order (router_row of x with itself); then every thread normalizes its four
+    // values in place. Every wavefront reading all of x from global memory for its own sum of squares instead
+    // takes ~8 us at this grid (2048 wavefronts on the same 64 lines).
+    static_assert(kFusedMaxHidden / 4 <= kFusedThreads, "one float4 of x per thread");
+    if constexpr (NORM) {
+        __shared__ float lds_inv;
+        const bool mine = static_cast<int>(threadIdx.x) < H / 4;
+        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), nw = xv;
+        if (mine) {
+            xv = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
+            if (a.norm_w) nw = reinterpret_cast<const float4*>(a.norm_w)[threadIdx.x];
+            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = xv;
+        }
+        __syncthreads();
+        if (wv == 0) {
+            const float ss = router_row(lds_xn, lds_xn, true, H, lane);
+            if (lane == 0) lds_inv = norm_inv(ss, H, a.norm_eps);
+        }
+        __syncthreads();
+        if (mine) reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = norm_apply(xv, a.norm_w != nullptr, nw, lds_inv);
+        __syncthreads();
+    }
     auto xload = [&](int i) -> float4 {
         if constexpr (NORM)
-            return norm_x(i);
+            return reinterpret_cast<const float4*>(lds_xn)[i];
         else
             return reinterpret_cast<const float4*>(a.x)[i];
     };
@@ -466,6 +487,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if (wv == kFusedWaves - 1 && owner && a.next_sh_down)
             touched ^= touch_lines(a.next_sh_down + static_cast<int64_t>(kOwnRows * b) * dn_rs,
                                    static_cast<int>(kOwnRows * dn_rs), lane);
+        if (wv == kFusedWaves - 2 && a.next_norm_w)  // every workgroup reads all of it first thing
+            touched ^= touch_lines(reinterpret_cast<const uint8_t*>(a.next_norm_w), 4 * H, lane);
     }
     if (owner && wv < k) {
         auto own_row = [&](int pass) { return kOwnRows * b + R * pass + drow; };
@@ -635,6 +658,7 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
         a.next_sh_gate = nx->shared_gate_up ? nx->shared_gate : nullptr;
         a.next_sh_gate_up = static_cast<const uint8_t*>(nx->shared_gate_up);
         a.next_sh_down = static_cast<const uint8_t*>(nx->shared_down);
+        a.next_norm_w = (nx->flags & WL_MOE_PRE_NORM) ? nx->norm_weight : nullptr;
     }
     void* args[] = {&a};
     const hipError_t e = hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a.G)), dim3(kFusedThreads), args, 0, s);

@@ -2,6 +2,7 @@
 and the weighted combine with the shared expert, all on the GPU with no host synchronization. This is
 Engine.moe (engines/base.py:445-490) without its `.cpu()` dispatch (:456-460).
 """
+import copy
 import ctypes
 
 import torch
@@ -73,7 +74,8 @@ class MoELayer:
         if pre_norm:
             s.flags |= MOE_PRE_NORM
             if norm_weight is not None:
-                self.norm_weight = torch.as_tensor(norm_weight).to(device=self.device, dtype=torch.float32).reshape(-1).contiguous()
+                self.norm_weight = torch.as_tensor(norm_weight).to(device=self.device,
+                                                                   dtype=torch.float32).reshape(-1).contiguous()
             s.norm_weight = _ptr(self.norm_weight)
             s.norm_eps = float(norm_eps)
         if residual:
@@ -96,6 +98,25 @@ class MoELayer:
                    shared_gate=dev(lw.get("shared_gate")), shared_inter=lw.get("shared_inter"),
                    shared_gate_up_type=lw.get("shared_gate_up_type"), shared_down_type=lw.get("shared_down_type"),
                    fused=fused, mfma=mfma, **kw)
+
+    def with_norm(self, norm_weight=None, norm_eps: float = 1e-6, residual: bool = True) -> "MoELayer":
+        """The same weights as one decoder step's MoE half, x + MoE(rms_norm(x)) (engines/qwen36/model.py:22):
+        a new layer object sharing this one's device tensors, with pre_norm set (and residual unless told not
+        to). Its next layer is unset."""
+        other = copy.copy(self)
+        other._ws, other._next = None, None
+        s = WlMoeLayer.from_buffer_copy(self.struct)
+        s.next = None
+        s.flags |= MOE_PRE_NORM | (MOE_RESIDUAL if residual else 0)
+        other.norm_weight = None
+        if norm_weight is not None:
+            other.norm_weight = torch.as_tensor(norm_weight).to(device=self.device,
+                                                                dtype=torch.float32).reshape(-1).contiguous()
+        s.norm_weight = _ptr(other.norm_weight)
+        s.norm_eps = float(norm_eps)
+        other.struct = s
+        check(library().wl_moe_check(ctypes.byref(s)))
+        return other
 
     def set_next(self, layer: "MoELayer" = None):
         """The layer the caller runs after this one (or None). With the same shapes, a batch-1 call pulls the rows
