@@ -1,7 +1,8 @@
 """A decode step captured once as a HIP graph and replayed (the way bench.py runs its 40 layers): every replay,
 with new inputs copied into the captured buffers and eager layer calls in between, gives exactly the eager result.
-Covers the three plans: fused (1 token), GEMV (2..8 tokens) and MFMA (more than 8). The layers record no
-memset nodes (their counters and flags are cleared by kernels)."""
+Covers the plans: fused (1 token), GEMV (2..8 tokens) and split (more than 8: at 40 tokens over 64 experts the
+GEMV experts run on the library's second stream, forked and joined by events, which capture turns into graph
+edges). The layers record no memset nodes (their counters and flags are cleared by kernels)."""
 import pytest
 import torch
 
