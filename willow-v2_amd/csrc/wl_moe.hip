@@ -1359,7 +1359,12 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     // MFMA expert, and the second stream's empty GEMV launches cost more than they overlap: 22.4 -> 22.7 ms per
     // 4096-token chunk)
     constexpr int64_t kForkMaxAvg = 32;
-    if (plan == kPlanSplit && may_fork && !events && P < kForkMaxAvg * L.n_experts) {
+    const bool few_gemv = plan == kPlanSplit && P >= kForkMaxAvg * L.n_experts;
+    // the GEMV launches' grid bound: at prefill sizes a GEMV expert is rare, and a grid sized for one per possible
+    // expert costs ~4.5 us per launch to dispatch and retire empty; one workgroup per CU loops over whatever items
+    // there are
+    const int gemv_slots = few_gemv && max_gemv > 8 ? 8 : max_gemv;
+    if (plan == kPlanSplit && may_fork && !events && !few_gemv) {
         fk = fork_streams(&rc);
         if (!fk) return rc;
         fork_guard = std::unique_lock<std::mutex>(g_fork_lock);
@@ -1372,7 +1377,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         rc = launch_mfma_gate_up(L, tokens, w, gemv_max, s);
         if (rc) return rc;
     }
-    launch_gemv_gate_up(L, ga, max_gemv, shared && !mfma, s_gemv);
+    launch_gemv_gate_up(L, ga, gemv_slots, shared && !mfma, s_gemv);
     rc = launch_status();
     if (rc) return rc;
     mark(4);
@@ -1380,7 +1385,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         rc = launch_mfma_down(L, tokens, w, gemv_max, s);
         if (rc) return rc;
     }
-    launch_gemv_down(L, ga, max_gemv, shared && !mfma, s_gemv);
+    launch_gemv_down(L, ga, gemv_slots, shared && !mfma, s_gemv);
     rc = launch_status();
     if (rc) return rc;
     if (fk) {  // join: the combine waits for the GEMV experts
