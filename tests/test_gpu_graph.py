@@ -40,3 +40,37 @@ def test_graph_replays_match_eager(layers, tokens):
         torch.cuda.synchronize()
         assert torch.isfinite(eager).all()
         assert torch.equal(y_out, eager), f"replay {rep}: max diff {(y_out - eager).abs().max().item()}"
+
+
+def test_split_fork_from_two_threads(layers):
+    """Split-plan calls from two host threads at once, each on its own stream: their GEMV experts share the
+    library's second stream (fork and join under one lock), and every result equals the same call made alone."""
+    import threading
+    tokens = 40
+    xs = [torch.from_numpy(synth.tokens(500 + i, tokens)).cuda() for i in range(2)]
+    want = [layers[i](xs[i]) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = [[None] * 6 for _ in range(2)]
+    errors = []
+
+    def worker(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                ws = new_workspace(layers[i].workspace_bytes(tokens), "cuda")
+                for r in range(6):
+                    outs[i][r] = layers[i](xs[i], workspace=ws)
+            streams[i].synchronize()
+        except Exception as e:  # reported below, in the test's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for i in range(2):
+        for r in range(6):
+            assert torch.equal(outs[i][r], want[i]), f"thread {i}, call {r}"
