@@ -37,8 +37,21 @@ struct NormX {
     }
 };
 
+// A router row's weights for router_row_xw: float4 i of 64-value segment s.
+struct GlobalRow {
+    const float* w;
+    __device__ __forceinline__ float4 operator()(int s, int i) const {
+        return reinterpret_cast<const float4*>(w + s * kRouterSeg)[i];
+    }
+};
+
+template <typename XF, typename WF>
+__device__ __forceinline__ float router_row_xw(XF x4, WF w4, bool valid, int H, int lane);
+
 template <typename XF>
-__device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ wr, bool valid, int H, int lane);
+__device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ wr, bool valid, int H, int lane) {
+    return router_row_xw(x4, GlobalRow{wr}, valid, H, lane);
+}
 
 __device__ __forceinline__ float router_row(const float* __restrict__ x, const float* __restrict__ wr, bool valid,
                                             int H, int lane) {
@@ -53,8 +66,8 @@ __device__ __forceinline__ float norm_inv(float s, int H, float eps) {
     return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s, static_cast<float>(H)), eps)));
 }
 
-template <typename XF>
-__device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ wr, bool valid, int H, int lane) {
+template <typename XF, typename WF>
+__device__ __forceinline__ float router_row_xw(XF x4, WF w4, bool valid, int H, int lane) {
     const int slot = lane & 31, src_base = lane & 32;
     const int nseg = H / kRouterSeg;
     float total = 0.0f;
@@ -64,10 +77,9 @@ __device__ __forceinline__ float router_row_x(XF x4, const float* __restrict__ w
         float p = 0.0f;
         const int s = slot + 32 * j;
         if (valid && s < nseg) {
-            const float4* wp = reinterpret_cast<const float4*>(wr + s * kRouterSeg);
 #pragma unroll
             for (int i = 0; i < kRouterSeg / 4; i++) {
-                const float4 wv = wp[i], xv = x4(s * (kRouterSeg / 4) + i);
+                const float4 wv = w4(s, i), xv = x4(s * (kRouterSeg / 4) + i);
                 p = __builtin_fmaf(xv.x, wv.x, p);
                 p = __builtin_fmaf(xv.y, wv.y, p);
                 p = __builtin_fmaf(xv.z, wv.z, p);

@@ -205,6 +205,18 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // values in place. Every wavefront reading all of x from global memory for its own sum of squares instead
     // takes ~8 us at this grid (2048 wavefronts on the same 64 lines).
     static_assert(kFusedMaxHidden / 4 <= kFusedThreads, "one float4 of x per thread");
+    static_assert(kFusedMaxHidden <= 32 * kRouterSeg, "a router row: one 64-value segment per lane of a half-wave");
+    // With NORM, a wavefront whose first phase-A task is a router row requests that row (lane s < 32: segment s)
+    // before the norm prologue, so its latency overlaps the wait for x instead of following the prologue.
+    float4 wpre[kRouterSeg / 4];
+    if constexpr (NORM) {
+        if (slot < n_logits && lane < H / kRouterSeg) {
+            const float* wr0 = slot < E ? a.router + static_cast<int64_t>(slot) * H : a.sh_gate;
+#pragma unroll
+            for (int i = 0; i < kRouterSeg / 4; i++)
+                wpre[i] = reinterpret_cast<const float4*>(wr0 + lane * kRouterSeg)[i];
+        }
+    }
     if constexpr (NORM) {
         __shared__ float lds_inv;
         const bool mine = static_cast<int>(threadIdx.x) < H / 4;
@@ -268,7 +280,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const int row = t;
             const bool valid = lane < 32;
             const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
-            const float total = router_row_x(xload, wr, valid, H, lane);
+            float total;
+            if (NORM && t == slot)  // the row requested before the norm prologue
+                total = router_row_xw(xload, [&](int, int i) { return wpre[i]; }, valid, H, lane);
+            else
+                total = router_row_x(xload, wr, valid, H, lane);
             if ((lane & 31) == 0 && valid && publish)
                 put_tagged(a.sync, kTagLogits + 2 * row, tag,
                            (row < E && a.router_bias) ? __fadd_rn(total, a.router_bias[row]) : total);
