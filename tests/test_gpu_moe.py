@@ -256,6 +256,21 @@ def test_prefill_mfma_variants(hip, variant):
     check_prefill(hip, layer, lw, synth.tokens(71, T, kw["hidden"]), variant)
 
 
+@pytest.mark.parametrize("T", [12, 64])
+def test_mfma_small_batches_k_split(hip, layer_c2, T):
+    """At most 64 tokens with every expert on the MFMA GEMMs (the full-shape layer): the K-split kernels, gate_up's
+    K over 4 wavefronts of a workgroup and down's over 2, whose partial sums are added in a fixed order through LDS.
+    12 tokens: every tile holds at most 16 tokens (one token tile); 64: tiles of up to 64 tokens, the shared
+    expert's among them. A second run gives the same bits."""
+    layer = hip.MoELayer.from_host(layer_c2, mfma="always")
+    assert layer.plan(T) == "mfma"
+    x = synth.tokens(900 + T, T)
+    check_prefill(hip, layer, layer_c2, x, f"c2 mfma b={T}")
+    y1, _, _ = run_layer(hip, layer, x)
+    y2, _, _ = run_layer(hip, layer, x)
+    np.testing.assert_array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
 def test_fused_give_up_is_reported(hip, layer_c2):
     """The fused kernel's hand-offs need every workgroup resident; a wait that runs out gives up rather than hang.
     Forced from the host (WL_MOE_TEST_STARVE: one workgroup withholds its results, the other waits give up after

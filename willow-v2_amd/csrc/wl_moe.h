@@ -137,7 +137,11 @@ inline int plan_gemv_max(ExpertPlan plan) {
 int max_tiles(const WlMoeLayer& L, int64_t T, int cap, int gemv_max);
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s);
-int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);
+// with_gemv: the call also has GEMV experts (a split plan), which may run beside this launch on a second stream;
+// the K-split gate_up kernel is then not used (its 128 KiB of LDS per workgroup keeps the GEMV workgroups off its
+// CUs). The choice depends on the plan alone, so every entry point runs the same kernels on the same call.
+int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
+                        hipStream_t s);
 int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);
 int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x, int64_t T, uint16_t* y,
                   hipStream_t s);

@@ -1378,7 +1378,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         s_gemv = fk->side;
     }
     if (mfma) {
-        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, s);
+        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, plan == kPlanSplit, s);
         if (rc) return rc;
     }
     launch_gemv_gate_up(L, ga, gemv_slots, shared && !mfma, s_gemv);

@@ -803,6 +803,194 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Calls of at most kKsTile tokens (batched decode). Every tile then holds at most 64 tokens, and the kernels above
+// give a tile's rows to few workgroups (one per 128 gate_up rows, per 512 down rows), each running the whole K
+// loop while most CUs idle. Here a workgroup takes fewer rows and splits their K loop over its wavefronts:
+// wavefront w = KQ rg + kq holds row group rg (kRT row tiles of 16) and computes the 256-value blocks kc with
+// kc % KQ == kq. Phase p stages the KQ chunks p KQ .. p KQ + KQ - 1 of the tile's activations at once, one LDS slot
+// each, and wavefront kq computes chunk p KQ + kq; the row states of its next chunk are requested as a phase
+// starts computing. After the last phase the KQ partial sums of a row group are added in kq order (a fixed order,
+// so results do not depend on timing) through LDS, and wavefront kq = 0 stores them.
+constexpr int kKsTile = 64;
+
+template <int TYPE, int NT, int KQ, typename RowPtr>
+__device__ __forceinline__ void gemm_ksplit(uint8_t* lds, floatx4 (&acc)[kRT][kKsTile / 16], int nblocks,
+                                            const uint8_t* src, const uint32_t* rowtab, RowPtr row_ptr, int lr,
+                                            int q) {
+    constexpr int NTA = kKsTile / 16;
+    constexpr int kChunk = NT * kGemmWaves * 1024;  // one chunk: NT token tiles of 16 tokens x 256 values
+    static_assert(NT <= NTA && kGemmWaves % KQ == 0, "");
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), half = lane >> 5;
+    const int kq = wv % KQ;
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 31) ^ ((2 * wv + half) & swizzle<TYPE>()));
+    const uint32_t lds0 = lds_address(lds);
+    const BAddr ba = b_addr<TYPE>(lr, q);
+    const int nphase = nblocks / KQ;
+    RowState<TYPE> rs[kRT], nx[kRT];
+#pragma unroll
+    for (int r = 0; r < kRT; r++) rs[r].fetch(row_ptr(r, lr) + static_cast<int64_t>(kq) * BlockInfo<TYPE>::bytes, q);
+    bf16x8 a0[kRT], a1[kRT], b[NT];
+    for (int p = 0; p < nphase; p++) {
+        if (p > 0) __syncthreads();  // every wavefront is done with the previous phase's chunks
+        for (int c = 0; c < KQ; c++)
+            stage_async<kKsTile, NT>(lds0 + c * kChunk, src + static_cast<int64_t>(p * KQ + c) * kTileRowBytes, rowtab,
+                                     col, wv, half);
+        wait_stage();  // the phase's chunks and this wavefront's row states have landed
+        __syncthreads();
+        if (p + 1 < nphase) {
+#pragma unroll
+            for (int r = 0; r < kRT; r++)
+                nx[r].fetch(row_ptr(r, lr) + static_cast<int64_t>((p + 1) * KQ + kq) * BlockInfo<TYPE>::bytes, q);
+        }
+        const uint8_t* buf = lds + kq * kChunk;
+        read_b<TYPE, NT, 0>(buf, ba, b);
+#pragma unroll
+        for (int r = 0; r < kRT; r++) {
+            rs[r].prepare(q);
+            a0[r] = rs[r].template frag<0>(q);
+        }
+        gemm_step<TYPE, NT, 0, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 1, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 2, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 3, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 4, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 5, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        gemm_step<TYPE, NT, 6, NTA>(buf, ba, rs, acc, a0, b, a1, q);
+        gemm_step<TYPE, NT, 7, NTA>(buf, ba, rs, acc, a1, b, a0, q);
+        if (p + 1 < nphase) {
+#pragma unroll
+            for (int r = 0; r < kRT; r++) rs[r] = nx[r];
+        }
+    }
+    // the partial sums of wavefronts kq > 0 cross through the (now free) staging slots
+    __syncthreads();
+    floatx4* red = reinterpret_cast<floatx4*>(lds);
+    const int rg = wv / KQ;
+    auto slot = [&](int j, int r, int n) { return (((rg * (KQ - 1) + j - 1) * kRT + r) * NT + n) * 64 + lane; };
+    if (kq > 0) {
+#pragma unroll
+        for (int r = 0; r < kRT; r++)
+#pragma unroll
+            for (int n = 0; n < NT; n++) red[slot(kq, r, n)] = acc[r][n];
+    }
+    __syncthreads();
+    if (kq == 0) {
+        for (int j = 1; j < KQ; j++) {
+#pragma unroll
+            for (int r = 0; r < kRT; r++)
+#pragma unroll
+                for (int n = 0; n < NT; n++) {
+                    const floatx4 v = red[slot(j, r, n)];
+                    acc[r][n] = floatx4{acc[r][n][0] + v[0], acc[r][n][1] + v[1], acc[r][n][2] + v[2],
+                                        acc[r][n][3] + v[3]};
+                }
+        }
+    }
+}
+
+// The tile's activation rows (src_row(t), t < count, for rows of ld values) into rowtab; then the K-split loop for
+// the fewest token tiles covering count (1 or 4).
+template <int TYPE, int KQ, typename RowPtr, typename SrcRow>
+__device__ __forceinline__ void gemm_tile_ks(uint8_t* lds, floatx4 (&acc)[kRT][kKsTile / 16], int nblocks,
+                                             int count, const uint16_t* __restrict__ src, int64_t ld, SrcRow src_row,
+                                             RowPtr row_ptr) {
+    __shared__ __attribute__((aligned(16))) uint32_t rowtab[kKsTile];
+    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+    for (int t = threadIdx.x; t < kKsTile; t += blockDim.x)
+        rowtab[rowtab_index<kKsTile>(t)] = static_cast<uint32_t>(src_row(t < count ? t : 0) * ld * 2);
+#pragma unroll
+    for (int r = 0; r < kRT; r++)
+#pragma unroll
+        for (int n = 0; n < kKsTile / 16; n++) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    const uint8_t* s8 = uniform_ptr(reinterpret_cast<const uint8_t*>(src));
+    if (count > 16)
+        gemm_ksplit<TYPE, 4, KQ>(lds, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+    else
+        gemm_ksplit<TYPE, 1, KQ>(lds, acc, nblocks, s8, rowtab, row_ptr, lr, q);
+}
+
+// gate_up, K split KQ ways: a workgroup takes kGemmWaves / KQ row groups, group rg the 16 gate rows
+// j0 = slab * kSlab + 16 rg .. + 15 and the matching up rows (kSlab = 16 kGemmWaves / KQ; the host passes the
+// number of such slabs of the widest intermediate dim in nslab_gate_up). Epilogue as k_gemm_gate_up's.
+template <int TYPE, int KQ>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up_ks(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[KQ * kKsTile * kTileRowBytes];
+    static_assert(kRT == 2, "one gate and one up row tile per wavefront");
+    constexpr int kSlab = 16 * kGemmWaves / KQ;
+    int slab, ti;
+    slab_tile(a.nslab_gate_up, slab, ti);
+    if (ti >= a.n_tiles[0]) return;
+    const int4 tile = a.tiles[ti];
+    const bool sh = tile.x == a.E;
+    const int inter = sh ? a.sh_inter : a.inter;
+    if (slab * kSlab >= inter) return;
+    const int wv = static_cast<int>(threadIdx.x >> 6), rg = wv / KQ, kq = wv % KQ;
+    const int j0 = slab * kSlab + 16 * rg;
+    const uint8_t* W = sh ? a.sh_gate_up : a.gate_up + static_cast<int64_t>(tile.x) * a.gate_up_stride;
+    const int nb = a.H / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const int pos0 = tile.y, count = tile.z;
+    floatx4 acc[kRT][kKsTile / 16];
+    auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>((r == 0 ? 0 : inter) + j0 + lr) * rs; };
+    auto src_row = [&](int t) -> int64_t { return sh ? pos0 + t : a.sorted[pos0 + t] / a.k; };
+    gemm_tile_ks<TYPE, KQ>(lds, acc, nb, count, a.xb, a.H, src_row, row_ptr);
+    if (kq != 0) return;
+    uint16_t* out = sh ? a.h_sh16 : a.h16;
+    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int n = 0; n < kKsTile / 16; n++) {
+        const int t = 16 * n + lr;
+        if (t < count) {
+            const floatx4 g = acc[0][n], u = acc[1][n];
+            *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * inter + j0 + 4 * q) =
+                make_uint2(swiglu_bf16(g[0], u[0], g[1], u[1]), swiglu_bf16(g[2], u[2], g[3], u[3]));
+        }
+    }
+}
+
+// down, K split KQ ways: a workgroup takes the kRows = 16 kRT kGemmWaves / KQ output rows group * kRows .. + kRows
+// - 1, row group rg the 16 kRT rows from group * kRows + 16 kRT rg. Epilogue as k_gemm_down's.
+template <int TYPE, int KQ>
+__global__ __launch_bounds__(kGemmThreads) void k_gemm_down_ks(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[KQ * kKsTile * kTileRowBytes];
+    constexpr int kRows = 16 * kRT * kGemmWaves / KQ;
+    int group, ti;
+    slab_tile(a.H / kRows, group, ti);
+    if (ti >= a.n_tiles_down[0]) return;
+    const int4 tile = a.tiles_down[ti];
+    const bool sh = tile.x == a.E;
+    const int inter = sh ? a.sh_inter : a.inter;
+    const int wv = static_cast<int>(threadIdx.x >> 6), rg = wv / KQ, kq = wv % KQ;
+    const int row0 = group * kRows + 16 * kRT * rg;
+    const uint8_t* W = sh ? a.sh_down : a.down + static_cast<int64_t>(tile.x) * a.down_stride;
+    const int nb = inter / kQK;
+    const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
+    const int pos0 = tile.y, count = tile.z;
+    floatx4 acc[kRT][kKsTile / 16];
+    auto row_ptr = [&](int r, int lr) { return W + static_cast<int64_t>(row0 + 16 * r + lr) * rs; };
+    auto src_row = [&](int t) -> int64_t { return pos0 + t; };
+    gemm_tile_ks<TYPE, KQ>(lds, acc, nb, count, sh ? a.h_sh16 : a.h16, inter, src_row, row_ptr);
+    if (kq != 0) return;
+    uint16_t* out = sh ? a.o_sh16 : a.o16;
+    const int64_t ldo = sh ? a.H : a.ldo;
+    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < kRT; r++) {
+#pragma unroll
+        for (int n = 0; n < kKsTile / 16; n++) {
+            const int t = 16 * n + lr;
+            if (t < count) {
+                const floatx4 v = acc[r][n];
+                *reinterpret_cast<uint2*>(out + static_cast<int64_t>(pos0 + t) * ldo + row0 + 16 * r + 4 * q) =
+                    make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s) {
@@ -883,10 +1071,35 @@ static int tiles8(const WlMoeLayer& L, int64_t T, int cap, int gemv_max) {
     return (max_tiles(L, T, cap, gemv_max) + kXcds - 1) / kXcds * kXcds;
 }
 
+// The K-split kernels' ways: gate_up (K = hidden) 4, down (K = the expert width) 2.
+constexpr int kKsGateUp = 4, kKsDown = 2;
+constexpr int kKsSlab = 16 * kGemmWaves / kKsGateUp;        // gate rows per k_gemm_gate_up_ks workgroup
+constexpr int kKsRows = 16 * kRT * kGemmWaves / kKsDown;    // output rows per k_gemm_down_ks workgroup
+
+// Whether a call runs the K-split kernels: at most kKsTile tokens (so every tile holds at most that many), and
+// shapes whose block counts divide into the ways and whose rows divide into the workgroups' row sets.
+static bool ks_eligible(const WlMoeLayer& L, int64_t T) {
+    if (T > kKsTile) return false;
+    auto inter_ok = [](int inter) { return inter % kKsSlab == 0 && (inter / kQK) % kKsDown == 0; };
+    return (L.hidden / kQK) % kKsGateUp == 0 && L.hidden % kKsRows == 0 && inter_ok(L.inter) &&
+           (!L.shared_gate_up || inter_ok(L.shared_inter));
+}
+
 // The MFMA experts' gate_up + SwiGLU (the routed experts with more than gemv_max pairs and the shared expert).
 // The routed and shared experts share one launch, so their types must agree (checked by prefill_eligible).
-int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s) {
-    const PrefillArgs a = prefill_args(L, T, w);
+int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
+                        hipStream_t s) {
+    PrefillArgs a = prefill_args(L, T, w);
+    if (ks_eligible(L, T) && !with_gemv) {
+        const int inter_max = a.sh_inter > a.inter ? a.sh_inter : a.inter;
+        a.nslab_gate_up = (inter_max + kKsSlab - 1) / kKsSlab;
+        const dim3 grid(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max)));
+        if (L.gate_up_type == WL_TYPE_Q4_K)
+            k_gemm_gate_up_ks<WL_TYPE_Q4_K, kKsGateUp><<<grid, kGemmThreads, 0, s>>>(a);
+        else
+            k_gemm_gate_up_ks<WL_TYPE_Q6_K, kKsGateUp><<<grid, kGemmThreads, 0, s>>>(a);
+        return launch_status();
+    }
     if (L.gate_up_type == WL_TYPE_Q4_K)
         k_gemm_gate_up<WL_TYPE_Q4_K, kTileTokens>
             <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max))), kGemmThreads, 0,
@@ -901,6 +1114,14 @@ int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int 
 // The MFMA experts' down products.
 int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s) {
     const PrefillArgs a = prefill_args(L, T, w);
+    if (ks_eligible(L, T)) {
+        const dim3 grid(static_cast<unsigned>(L.hidden / kKsRows * tiles8(L, T, kDownTileTokens, gemv_max)));
+        if (L.down_type == WL_TYPE_Q4_K)
+            k_gemm_down_ks<WL_TYPE_Q4_K, kKsDown><<<grid, kGemmThreads, 0, s>>>(a);
+        else
+            k_gemm_down_ks<WL_TYPE_Q6_K, kKsDown><<<grid, kGemmThreads, 0, s>>>(a);
+        return launch_status();
+    }
     const dim3 g2(static_cast<unsigned>(L.hidden / 256 / a.down_slabs * tiles8(L, T, kDownTileTokens, gemv_max)));
     if (L.down_type == WL_TYPE_Q4_K)
         k_gemm_down<WL_TYPE_Q4_K><<<g2, kGemmThreads, 0, s>>>(a);
