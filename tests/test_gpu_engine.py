@@ -87,3 +87,36 @@ def test_store_surface(small_layer):
         assert off == e * lw["gate_up"][0].nbytes
     store.record_usage(0, torch.tensor([[3, 17], [3, 5]]))
     assert int(store.usage[0][3]) == 2
+
+
+def rms_norm_zero_centered(x, w, eps=1e-6):
+    """engines/base.py:27-31 with zero_centered (Qwen3.5's norm, engines/qwen36/model.py:37), in torch fp32."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * (1 + w)
+
+
+@pytest.mark.parametrize("tokens", [1, 9])
+def test_engine_model_loop(tokens):
+    """The MoE half of the decoder loop as engines/qwen36/model.py:22 runs it, x = x + moe(rms_norm(x), layer,
+    residual=x), over three layers of one HBMExpertStore through HipMoE.moe: each layer names the next (the
+    next-layer overlap), and the layer cache is built once. Each layer's output is checked against the oracle on
+    the same normalized input the engine got (so the check cannot depend on how torch orders the norm's sums)."""
+    lws = [synth.moe_layer(81 + l, hidden=2048, inter=512, shared_inter=512, experts=64, top_k=8) for l in range(3)]
+    store = HBMExpertStore.from_host(lws)
+    weights = {}
+    for l, lw in enumerate(lws):
+        weights.update(engine_weights(lw, layer=l))
+    eng = TinyEngine(store, weights, 8)
+    rng = np.random.default_rng(90)
+    norm_w = [torch.from_numpy(rng.normal(0, 0.1, 2048).astype(np.float32)).cuda() for _ in lws]
+    x = torch.from_numpy(synth.tokens(91 + tokens, tokens)).cuda()
+    for l, lw in enumerate(lws):
+        print(f"[engine] model loop T={tokens} layer {l}", flush=True)
+        xn = rms_norm_zero_centered(x, norm_w[l])
+        y = eng.moe(xn, l, residual=x)
+        ref = moe_ref.layer(xn.cpu().numpy(), lw, chain="split", dtype=np.float64)
+        assert moe_ref.rel_err(y.cpu().numpy(), ref) < 2e-3
+        x = x + y
+    views = eng.__dict__["_hip_moe_layers"]
+    assert sorted(views) == [0, 1, 2]
+    assert views[0][0]._next is views[1][0] and views[1][0]._next is views[2][0]
+    assert torch.isfinite(x).all()
