@@ -669,23 +669,31 @@ __global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a, int rows, int chu
     extern __shared__ __attribute__((aligned(16))) float lds_x[];
     constexpr int JW = 32 / L, JG = 4 * JW;
     const int groups = (rows + JG - 1) / JG;
-    const int items = expert_slots(a) * groups;
+    // an item is (token chunk index tc, slot, row group), tc outermost: a slot's chunks go to different
+    // workgroups, so one with 8 tokens is not a single item taking twice as long as the rest (chunks tc,
+    // tc + nc, ... when a slot holds more than kGemvTok tokens)
+    const int nc = (kGemvTok + chunk - 1) / chunk;
+    const int per_c = expert_slots(a) * groups;
+    const int items = per_c * nc;
     const int lane = threadIdx.x & 63, c = lane % L, rw = (lane & 31) / L;
     const bool up_half = lane >= 32;
     const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nb = a.H / kQK;
     const int64_t rs = static_cast<int64_t>(nb) * BlockInfo<TYPE>::bytes;
     const int ldx = lds_row_floats(a.H), ldsum = a.H / 16;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int tc = item / per_c, it = item - tc * per_c;
         const int slot = it / groups;
         const ExpertView v = expert_view(a, slot, true);
+        const int first = v.begin + tc * chunk;
+        if (first >= v.end) continue;  // whole workgroup: the slot has fewer chunks
         const int inter = static_cast<int>(v.stride_rows);
         const int j = (it - slot * groups) * JG + wv * JW + rw;
         const uint8_t* wrow = v.w + static_cast<int64_t>((up_half ? inter : 0) + min(j, inter - 1)) * rs;
         float* hout = v.routed ? a.h : a.h_sh;
         BlockDot<TYPE> blk;
         blk.fetch(wrow + c * BlockInfo<TYPE>::bytes);  // the first block's loads overlap the staging below
-        for (int p0 = v.begin; p0 < v.end; p0 += chunk) {
+        for (int p0 = first; p0 < v.end; p0 += nc * chunk) {
             const int n = min(chunk, v.end - p0);
             __syncthreads();  // the previous chunk's LDS rows are no longer read
             stage_chunk(lds_x, n, a.H, [&](int u) {
@@ -697,7 +705,7 @@ __global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a, int rows, int chu
 #pragma unroll
             for (int u = 0; u < kGemvTok; u++) acc[u] = 0.0f;
             for (int kb = c; kb < nb; kb += L) {
-                if (kb != c || p0 != v.begin) blk.fetch(wrow + kb * BlockInfo<TYPE>::bytes);
+                if (kb != c || p0 != first) blk.fetch(wrow + kb * BlockInfo<TYPE>::bytes);
                 blk.run(lds_x + kb * kBlkFloats, ldx, lds_x + n * ldx + 16 * kb, ldsum, n, acc);
             }
 #pragma unroll
@@ -1089,8 +1097,9 @@ static unsigned gemv_grid(int64_t items) {
 template <int TYPE, int L>
 static void launch_gate_up_l(const ExpertArgs& a, int rows, int max_slots, hipStream_t s) {
     constexpr int JG = 4 * (32 / L);
-    const unsigned grid = gemv_grid(static_cast<int64_t>(max_slots) * ((rows + JG - 1) / JG));
     const int chunk = gemv_chunk(a.H);
+    const unsigned grid =
+        gemv_grid(static_cast<int64_t>(max_slots) * ((rows + JG - 1) / JG) * ((kGemvTok + chunk - 1) / chunk));
     k_gate_up<TYPE, L><<<grid, 256, sizeof(float) * chunk * lds_chunk_floats(a.H), s>>>(a, rows, chunk);
 }
 
