@@ -226,17 +226,20 @@ __device__ __forceinline__ void fetch_q4k(const uint8_t* __restrict__ blk, int q
 }
 
 // The scales of sub-blocks j = 2 q + e (q4k_scale_min with a per-lane j): j < 4 for q < 2, j >= 4 otherwise, and
-// the byte holding j's fields sits 8 ((2 q + e) & 3) bits into its word either way.
+// the byte holding j's fields sits 8 ((2 q + e) & 3) bits into its word either way. Both cases as one expression
+// with per-lane shift and masks (j < 4: s0 & 63, s1 & 63; j >= 4: the low 4 bits from s2 and bits 4, 5 from the top
+// of s0 / s1), so the wavefront does not branch on its lane groups.
 __device__ __forceinline__ void prepare_q4k(Q4KRowState& s, int q) {
     const float d = half_to_float(s.hd.x), dmin = half_to_float(s.hd.x >> 16);
     const bool hi = q >= 2;
+    const uint32_t sh_hi = hi ? 2u : 0u, mask_top = hi ? 0x30u : 0x3Fu, mask_low = hi ? 0xFu : 0u;
     const uint32_t sh0 = 16u * static_cast<uint32_t>(q & 1);
 #pragma unroll
     for (int e = 0; e < 2; e++) {
         const uint32_t sh = sh0 + 8u * e;
         const uint32_t s0 = s.hd.y >> sh, s1 = s.hd.z >> sh, s2 = s.hd.w >> sh;
-        const uint32_t sc = hi ? ((s2 & 0xFu) | ((s0 >> 2) & 0x30u)) : (s0 & 63u);
-        const uint32_t m = hi ? (((s2 >> 4) & 0xFu) | ((s1 >> 2) & 0x30u)) : (s1 & 63u);
+        const uint32_t sc = ((s0 >> sh_hi) & mask_top) | (s2 & mask_low);
+        const uint32_t m = ((s1 >> sh_hi) & mask_top) | ((s2 >> 4) & mask_low);
         s.a[e] = d * static_cast<float>(sc);
         s.b[e] = -(dmin * static_cast<float>(m));
     }
