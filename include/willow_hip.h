@@ -179,9 +179,9 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
  * weight * down(silu(gate x) * (up x)), plus sigmoid(x . shared_gate) * shared_down(silu(...) * (...)).
  * ids/weights (optional, may be NULL) receive the routing. Replaces engines/base.py:445-490 (Engine.moe) with its
  * dispatch (:456-467, :492-591) kept on the device: no host synchronization. In the split plan (wl_moe_plan() ==
- * 2), while the experts average fewer than 32 tokens, the experts on the GEMV kernels run on a second stream of the
- * device (created on the first such call and kept), forked from and joined back to `stream` by two events; under
- * stream capture both become graph edges. */
+ * 2), while the experts average fewer than 32 tokens, the experts on the MFMA GEMMs run on a second stream of the
+ * device (created on the first such call and kept) beside the GEMV experts on `stream`, forked from and joined back
+ * to `stream` by two events; under stream capture both become graph edges. */
 int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
                  void* workspace, size_t workspace_bytes, void* stream);
 

@@ -138,8 +138,9 @@ int max_tiles(const WlMoeLayer& L, int64_t T, int cap, int gemv_max);
 int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* logits, float* sg, uint16_t* xb,
                         hipStream_t s);
 // with_gemv: the call also has GEMV experts (a split plan), which may run beside this launch on a second stream;
-// the K-split gate_up kernel is then not used (its 128 KiB of LDS per workgroup keeps the GEMV workgroups off its
-// CUs). The choice depends on the plan alone, so every entry point runs the same kernels on the same call.
+// the K-split gate_up kernel then splits K 2 ways instead of 4 (64 KiB of LDS per workgroup instead of 128, which
+// kept the GEMV workgroups off its CUs). The choice depends on the plan alone, so every entry point runs the same
+// kernels on the same call.
 int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
                         hipStream_t s);
 int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);

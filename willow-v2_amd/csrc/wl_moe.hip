@@ -1261,13 +1261,16 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
 }
 
 
-// The split plan's two expert sets are disjoint until the combine, so wl_moe_layer runs the GEMV experts on a
-// second stream of the device beside the MFMA experts (64 tokens with Zipf(1.1) routing: 131 -> 100 us per layer): fork (an event on the caller's stream that the second stream
-// waits for), the GEMV kernels on the second stream, join (an event there that the caller's stream waits for).
-// Both chains are latency-bound and leave most of the GPU idle. The stream and events are created on a device's
-// first split call and kept; the whole fork-to-join sequence runs under one lock, so concurrent calls from several
-// host threads stay correct (their GEMV work queues on the one second stream). Under graph capture the fork and
-// join become graph edges.
+// The split plan's two expert sets are disjoint until the combine, so wl_moe_layer runs the MFMA experts on a
+// second stream of the device beside the GEMV experts (64 tokens with Zipf(1.1) routing: 131 -> 100 us per layer):
+// fork (an event on the caller's stream that the second stream waits for), the MFMA kernels on the second stream,
+// join (an event there that the caller's stream waits for). Both chains are latency-bound and leave most of the
+// GPU idle. The branch that waits for the fork and is waited for at the join starts and ends later than the
+// caller's, so it gets the shorter chain: the MFMA experts with the K-split gate_up (at 64 tokens 96.0 -> 95.0 us
+// per layer against the GEMV experts there). The stream and events are created on a device's first split call and
+// kept; the whole fork-to-join sequence runs under one lock, so concurrent calls from several host threads stay
+// correct (their MFMA work queues on the one second stream). Under graph capture the fork and join become graph
+// edges.
 struct ForkStreams {
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
@@ -1364,8 +1367,8 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     const int max_gemv = plan == kPlanMfma ? 0 : static_cast<int>(P < L.n_experts ? P : L.n_experts);
     // the shared expert runs on the MFMA GEMMs in an MFMA plan (it sees every token), else on the GEMV kernels
     const ExpertArgs ga = gemv_args(L, x, tokens, w, max_gemv, shared && !mfma);
-    // the GEMV experts' stream: the caller's, or with a split plan (and no stage events) the device's second stream
-    hipStream_t s_gemv = s;
+    // the MFMA experts' stream: the caller's, or with a split plan (and no stage events) the device's second stream
+    hipStream_t s_mfma = s;
     const ForkStreams* fk = nullptr;
     std::unique_lock<std::mutex> fork_guard;
     // worth it while the experts average fewer than kForkMaxAvg tokens (at prefill sizes nearly every expert is an
@@ -1384,25 +1387,25 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         hipError_t e = hipEventRecord(fk->fork, s);
         if (e == hipSuccess) e = hipStreamWaitEvent(fk->side, fk->fork, 0);
         if (e != hipSuccess) return static_cast<int>(e);
-        s_gemv = fk->side;
+        s_mfma = fk->side;
     }
     if (mfma) {
-        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, plan == kPlanSplit, s);
+        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, plan == kPlanSplit, s_mfma);
         if (rc) return rc;
     }
-    launch_gemv_gate_up(L, ga, gemv_slots, shared && !mfma, s_gemv);
+    launch_gemv_gate_up(L, ga, gemv_slots, shared && !mfma, s);
     rc = launch_status();
     if (rc) return rc;
     mark(4);
     if (mfma) {
-        rc = launch_mfma_down(L, tokens, w, gemv_max, s);
+        rc = launch_mfma_down(L, tokens, w, gemv_max, s_mfma);
         if (rc) return rc;
     }
-    launch_gemv_down(L, ga, gemv_slots, shared && !mfma, s_gemv);
+    launch_gemv_down(L, ga, gemv_slots, shared && !mfma, s);
     rc = launch_status();
     if (rc) return rc;
-    if (fk) {  // join: the combine waits for the GEMV experts
-        hipError_t e = hipEventRecord(fk->join, s_gemv);
+    if (fk) {  // join: the combine waits for the MFMA experts
+        hipError_t e = hipEventRecord(fk->join, s_mfma);
         if (e == hipSuccess) e = hipStreamWaitEvent(s, fk->join, 0);
         if (e != hipSuccess) return static_cast<int>(e);
         fork_guard.unlock();

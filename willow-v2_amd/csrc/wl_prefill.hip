@@ -1074,18 +1074,36 @@ static int tiles8(const WlMoeLayer& L, int64_t T, int cap, int gemv_max) {
     return (max_tiles(L, T, cap, gemv_max) + kXcds - 1) / kXcds * kXcds;
 }
 
-// The K-split kernels' ways: gate_up (K = hidden) 4, down (K = the expert width) 2.
-constexpr int kKsGateUp = 4, kKsDown = 2;
-constexpr int kKsSlab = 16 * kGemmWaves / kKsGateUp;        // gate rows per k_gemm_gate_up_ks workgroup
-constexpr int kKsRows = 16 * kRT * kGemmWaves / kKsDown;    // output rows per k_gemm_down_ks workgroup
+// The K-split kernels' ways: gate_up (K = hidden) 4, or 2 when GEMV experts run beside it (half the LDS per
+// workgroup, 64 KiB, so the GEMV workgroups still find room on its CUs), down (K = the expert width) 2.
+constexpr int kKsGateUp = 4, kKsGateUpBeside = 2, kKsDown = 2;
+template <int KQ>
+constexpr int ks_slab() { return 16 * kGemmWaves / KQ; }  // gate rows per k_gemm_gate_up_ks<., KQ> workgroup
+constexpr int kKsRows = 16 * kRT * kGemmWaves / kKsDown;  // output rows per k_gemm_down_ks workgroup
 
 // Whether a call runs the K-split kernels: at most kKsTile tokens (so every tile holds at most that many), and
-// shapes whose block counts divide into the ways and whose rows divide into the workgroups' row sets.
+// shapes whose block counts divide into the ways and whose rows divide into the workgroups' row sets (the larger
+// gate_up slab, of the 2-way kernel, is a multiple of the other).
 static bool ks_eligible(const WlMoeLayer& L, int64_t T) {
+    static_assert(ks_slab<kKsGateUpBeside>() % ks_slab<kKsGateUp>() == 0 && kKsGateUp % kKsGateUpBeside == 0, "");
     if (T > kKsTile) return false;
-    auto inter_ok = [](int inter) { return inter % kKsSlab == 0 && (inter / kQK) % kKsDown == 0; };
+    auto inter_ok = [](int inter) {
+        return inter % ks_slab<kKsGateUpBeside>() == 0 && (inter / kQK) % kKsDown == 0;
+    };
     return (L.hidden / kQK) % kKsGateUp == 0 && L.hidden % kKsRows == 0 && inter_ok(L.inter) &&
            (!L.shared_gate_up || inter_ok(L.shared_inter));
+}
+
+template <int KQ>
+static int launch_gate_up_ks(const WlMoeLayer& L, int64_t T, PrefillArgs a, int gemv_max, hipStream_t s) {
+    const int inter_max = a.sh_inter > a.inter ? a.sh_inter : a.inter;
+    a.nslab_gate_up = (inter_max + ks_slab<KQ>() - 1) / ks_slab<KQ>();
+    const dim3 grid(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max)));
+    if (L.gate_up_type == WL_TYPE_Q4_K)
+        k_gemm_gate_up_ks<WL_TYPE_Q4_K, KQ><<<grid, kGemmThreads, 0, s>>>(a);
+    else
+        k_gemm_gate_up_ks<WL_TYPE_Q6_K, KQ><<<grid, kGemmThreads, 0, s>>>(a);
+    return launch_status();
 }
 
 // The MFMA experts' gate_up + SwiGLU (the routed experts with more than gemv_max pairs and the shared expert).
@@ -1093,16 +1111,9 @@ static bool ks_eligible(const WlMoeLayer& L, int64_t T) {
 int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
                         hipStream_t s) {
     PrefillArgs a = prefill_args(L, T, w);
-    if (ks_eligible(L, T) && !with_gemv) {
-        const int inter_max = a.sh_inter > a.inter ? a.sh_inter : a.inter;
-        a.nslab_gate_up = (inter_max + kKsSlab - 1) / kKsSlab;
-        const dim3 grid(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max)));
-        if (L.gate_up_type == WL_TYPE_Q4_K)
-            k_gemm_gate_up_ks<WL_TYPE_Q4_K, kKsGateUp><<<grid, kGemmThreads, 0, s>>>(a);
-        else
-            k_gemm_gate_up_ks<WL_TYPE_Q6_K, kKsGateUp><<<grid, kGemmThreads, 0, s>>>(a);
-        return launch_status();
-    }
+    if (ks_eligible(L, T))
+        return with_gemv ? launch_gate_up_ks<kKsGateUpBeside>(L, T, a, gemv_max, s)
+                         : launch_gate_up_ks<kKsGateUp>(L, T, a, gemv_max, s);
     if (L.gate_up_type == WL_TYPE_Q4_K)
         k_gemm_gate_up<WL_TYPE_Q4_K, kTileTokens>
             <<<dim3(static_cast<unsigned>(a.nslab_gate_up * tiles8(L, T, kTileTokens, gemv_max))), kGemmThreads, 0,
