@@ -43,8 +43,10 @@ extern "C" {
 #define WL_EINVAL_DTYPE -7     /* output dtype is not WL_DTYPE_F32 / WL_DTYPE_BF16 */
 #define WL_EINVAL_COUNT -8     /* too many experts for one batched call */
 #define WL_EINVAL_SCRATCH -9   /* wl_moe_layer_noalloc: the call needs more than WL_NOALLOC_SCRATCH_BYTES */
-#define WL_ESYNC -10           /* wl_moe_workspace_status: a fused-kernel wait gave up since the last query */
+#define WL_ESYNC -10           /* wl_moe_workspace_status: a bounded wait gave up since the last query */
 #define WL_EINVAL_OVERLAP -11  /* wl_moe_layer: y overlaps x */
+#define WL_EINVAL_SCOPE -12    /* wl_moe_fork_begin with a scope open on the device; wl_moe_fork_end without one on
+                                  this stream */
 
 #define WL_MAX_TOPK 16
 #define WL_MAX_BATCH_EXPERTS 64 /* experts per wl_gemv_batch / wl_gemv_combine call */
@@ -139,10 +141,12 @@ int wl_moe_check(const WlMoeLayer* layer);
 /* Bytes of device workspace wl_moe_layer needs for `tokens` tokens (0 on an invalid layer). */
 size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
 
-/* The fused kernel's health since the previous query on this workspace (NULL: the current device's
- * wl_moe_layer_noalloc scratch). Its hand-offs between workgroups need the whole grid resident at once; the
- * library checks that before it launches, and every wait is bounded, so a workgroup that still waits too long gives
- * up, writes NaN for its outputs and sets a status word. This synchronizes `stream`, reads and clears the word, and
+/* The workspace's health since the previous query (NULL: the current device's wl_moe_layer_noalloc scratch).
+ * The fused kernel's hand-offs between workgroups need the whole grid resident at once; the library checks that
+ * before it launches, and every wait is bounded, so a workgroup that still waits too long gives up, writes NaN for
+ * its outputs and sets a status word. The waits of a fork scope (wl_moe_fork_begin) are bounded too; one that
+ * gives up sets the word, and until it is cleared the scope's MFMA experts are skipped (their outputs are stale).
+ * This synchronizes `stream` (and, after a fork-scope wait gave up, the device), reads and clears the word, and
  * returns WL_OK, WL_ESYNC when it was set, or a hipError_t. Not for use under stream capture. */
 int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
@@ -184,6 +188,21 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
  * to `stream` by two events; under stream capture both become graph edges. */
 int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* A fork scope on `stream` (the current device): wl_moe_fork_begin forks the device's second stream from `stream`
+ * once, wl_moe_fork_end joins it back once, and the split-plan wl_moe_layer calls on `stream` in between hand their
+ * MFMA experts to the second stream and back through words of their workspaces (set and polled by the kernels)
+ * instead of a fork and a join event each. Under stream capture that is two graph edges for a whole decode step of
+ * layers instead of two per layer (64 tokens with Zipf(1.1) routing, 40 layers: ~10 us per layer). One scope per
+ * device at a time, begun and ended on the same stream, with every call in it issued from one host thread in
+ * order; the workspaces must have been prepared by wl_moe_workspace_init. Between the calls the caller may run
+ * other work on `stream` (a model's attention), as long as each call's grouping follows the previous call's within
+ * the bounded wait (on the order of 100 ms); a wait that gives up is reported by wl_moe_workspace_status. Calls on
+ * other streams fork and join per call as outside a scope. No counterpart in the reference, which launches its
+ * experts from the host per layer (engines/base.py:515); the callers it is for are step-level graphs of layers
+ * (engines/base.py:392-406 overlaps the next layer's expert reads for the same purpose). */
+int wl_moe_fork_begin(void* stream);
+int wl_moe_fork_end(void* stream);
 
 /* wl_moe_layer with a hipEvent_t recorded on `stream` at every stage boundary: events_host[i] just before stage i,
  * events_host[wl_moe_stage_count()] after the last (so wl_moe_stage_count() + 1 events, none NULL). On the fused

@@ -29,9 +29,17 @@ constexpr int kFlagStride = 32;       // words between workgroups' epoch counter
 constexpr int kTagLogits = kFlagStride * kFusedMaxG;
 constexpr int kTagHsh = kTagLogits + 2 * (kFusedMaxE + 16);
 constexpr int kTagH = kTagHsh + 2 * kFusedMaxInter;
-// then the status word: nonzero once a fused-kernel workgroup's bounded wait gave up (wl_moe_workspace_status)
+// then the status word: nonzero once a bounded wait gave up (wl_moe_workspace_status); bit 0 a fused-kernel
+// workgroup's, bit 1 a fork-scope hand-off's (sticky: while it is set the scope's MFMA kernels do nothing)
 constexpr int kStatusWord = kTagH + 2 * kFusedMaxK * kFusedMaxInter;
-constexpr int kSyncWords = kStatusWord + kFlagStride;
+constexpr uint32_t kStatusFused = 1u, kStatusFork = 2u;
+// then, each on a line of its own, the fork-scope hand-off words of a split-plan call (wl_moe_fork_begin): the
+// grouping is done (1, set by the grouping, cleared by the second stream's wait), the MFMA experts are done (1, set
+// on the second stream, cleared by the grouping), and the MFMA kernels' skip word (1 after a wait gave up)
+constexpr int kForkSorted = kStatusWord + kFlagStride;
+constexpr int kForkDone = kForkSorted + kFlagStride;
+constexpr int kForkSkip = kForkDone + kFlagStride;
+constexpr int kSyncWords = kForkSkip + kFlagStride;
 
 struct ExpertArgs {
     const uint8_t* gate_up;
@@ -86,6 +94,7 @@ struct PrefillArgs {
     int nslab_gate_up;       // 128-row slabs of the widest intermediate dim
     int down_slabs;          // 256-row slabs per down workgroup
     int dense_tokens;        // > 0: k_gemm_down runs one matrix (down) over this many tokens, tiles implied
+    const uint32_t* skip;    // in a fork scope: nonzero when the wait for the grouping gave up (the kernel returns)
 };
 
 struct Workspace {
@@ -142,8 +151,10 @@ int launch_router_tiled(const WlMoeLayer& L, const float* x, int64_t T, float* l
 // kept the GEMV workgroups off its CUs). The choice depends on the plan alone, so every entry point runs the same
 // kernels on the same call.
 int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
-                        hipStream_t s);
-int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s);
+                        const uint32_t* skip, hipStream_t s);
+// skip (nullable): the fork-scope skip word, which the kernels read first (a nonzero value: they do nothing)
+int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, const uint32_t* skip,
+                     hipStream_t s);
 int launch_linear(int type, const uint8_t* w, int rows, int k, const uint16_t* x, int64_t T, uint16_t* y,
                   hipStream_t s);
 

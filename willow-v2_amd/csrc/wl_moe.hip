@@ -322,11 +322,62 @@ __device__ void tile_list(int4* __restrict__ tiles, int32_t* __restrict__ n_tile
     if (threadIdx.x == 0) n_tiles[0] = total + (with_shared ? (T + cap - 1) / cap : 0);
 }
 
+// Fork scope (wl_moe_fork_begin): the split plan's MFMA experts run on the device's second stream and meet the
+// caller's stream through words of the call's workspace instead of a fork and a join event per call. The grouping
+// publishes its results (kForkSorted = 1, after clearing kForkDone); the second stream's k_fork_wait waits for that
+// and clears it, then the MFMA kernels run and k_fork_store sets kForkDone = 1; the combine waits for kForkDone.
+// A word is only set after the one that clears it has been waited for, so the words need no epochs: the grouping's
+// clearing of kForkDone comes after the previous call's combine (the caller's stream), and the next kForkSorted
+// after the previous call's k_fork_wait cleared it (which the previous kForkDone, and so this grouping, waited
+// for). Every wait is bounded; one that gives up sets kStatusFork in the status word, after which every k_fork_wait
+// sets the skip word, so the MFMA kernels never read a grouping that is not there (wl_moe_workspace_status reports
+// WL_ESYNC and clears the words).
+
+// The grouping's results in memory for every agent, then the flags: every wavefront waits for its own stores to
+// land in the L2, and one thread's release store writes the L2 back once.
+__device__ __forceinline__ void publish_grouping(uint32_t* sync, int withhold) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(sync + kForkDone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!withhold) __hip_atomic_store(sync + kForkSorted, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// *a = va (when a), then *b = vb with release (when b); one thread, after the kernels before it on the stream.
+__global__ __launch_bounds__(64) void k_fork_store(uint32_t* a, uint32_t va, uint32_t* b, uint32_t vb) {
+    if (threadIdx.x != 0) return;
+    if (a) __hip_atomic_store(a, va, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (b) __hip_atomic_store(b, vb, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The second stream's wait for the grouping (one thread; at most spin_limit polls). Relaxed polls: an acquire
+// would invalidate this XCD's L2 on every poll under the kernels of the caller's stream; the MFMA kernels that
+// read the grouping are dispatched after this kernel ends and acquire at their start.
+__global__ __launch_bounds__(64) void k_fork_wait(uint32_t* sync, uint32_t spin_limit) {
+    if (threadIdx.x != 0) return;
+    uint32_t* sorted = sync + kForkSorted;
+    bool ok = (__hip_atomic_load(sync + kStatusWord, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kStatusFork) == 0;
+    for (uint32_t spins = 0; ok && __hip_atomic_load(sorted, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 1u;
+         spins++) {
+        if (spins >= spin_limit)
+            ok = false;
+        else
+            __builtin_amdgcn_s_sleep(1);
+    }
+    if (ok)
+        __hip_atomic_store(sorted, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        __hip_atomic_fetch_or(sync + kStatusWord, kStatusFork, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(sync + kForkSkip, ok ? 0u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t* __restrict__ ids, int T, int k,
                                                                   int E, int32_t* __restrict__ offsets,
                                                                   int32_t* __restrict__ active,
                                                                   int32_t* __restrict__ sorted,
-                                                                  int32_t* __restrict__ pair_pos, TileOut to) {
+                                                                  int32_t* __restrict__ pair_pos, TileOut to,
+                                                                  uint32_t* fork_sync, int withhold) {
     __shared__ int32_t lds_ids[kSortChunk * WL_MAX_TOPK];
     __shared__ uint32_t bits[kSortWords * 64 * kMaxEJ];  // expert e: words kSortWords e .. + kSortWords - 1
     __shared__ uint32_t lds_off[64 * kMaxEJ];  // first sorted position | kPosBf16 for an MFMA expert
@@ -369,6 +420,7 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
         tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
         tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
     }
+    if (fork_sync) publish_grouping(fork_sync, withhold);
 }
 
 // Many chunks: one thread per expert turns its per-chunk counts (hist[c][e]) into the chunk's first sorted
@@ -863,7 +915,23 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
                                                  const int32_t* __restrict__ pair_pos,
                                                  const float* __restrict__ wts, const float* __restrict__ o,
                                                  const SH* __restrict__ o_sh, const float* __restrict__ sg,
-                                                 const float* __restrict__ resid, float* __restrict__ y) {
+                                                 const float* __restrict__ resid, float* __restrict__ y,
+                                                 uint32_t* fork_sync, uint32_t spin_limit) {
+    if (fork_sync) {  // fork scope: the MFMA experts' outputs come from the second stream (at most spin_limit
+                      // relaxed polls, then one acquire for the workgroup's reads)
+        if (threadIdx.x == 0) {
+            bool ok = false;
+            for (uint32_t spins = 0; spins < spin_limit && !ok; spins++) {
+                ok = __hip_atomic_load(fork_sync + kForkDone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+                if (!ok) __builtin_amdgcn_s_sleep(1);
+            }
+            if (!ok)
+                __hip_atomic_fetch_or(fork_sync + kStatusWord, kStatusFork, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_SYSTEM);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        __syncthreads();
+    }
     const int spans = (H + kCombineSpan - 1) / kCombineSpan;
     const int t = static_cast<int>(blockIdx.x) / spans;
     const int r = (static_cast<int>(blockIdx.x) - t * spans) * kCombineSpan + 8 * static_cast<int>(threadIdx.x);
@@ -1066,15 +1134,16 @@ static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int3
     return launch_status();
 }
 
-// The grouping; with an MFMA plan (tiles) also the tile lists of the experts with more than gemv_max pairs.
+// The grouping; with an MFMA plan (tiles) also the tile lists of the experts with more than gemv_max pairs; in a
+// fork scope (fork) it then publishes itself to the second stream (withhold: WL_MOE_TEST_STARVE, it does not).
 static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* ids, int64_t T, bool tiles,
-                       int gemv_max, hipStream_t s) {
+                       int gemv_max, bool fork, bool withhold, hipStream_t s) {
     const int E = L.n_experts, k = L.top_k;
     const TileOut to{tiles ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0, gemv_max};
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
     if (nchunks == 1) {
         k_sort_small<<<1, kSortSmallThreads, 0, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted,
-                                                     w.pair_pos, to);
+                                                     w.pair_pos, to, fork ? w.sync : nullptr, withhold ? 1 : 0);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
         k_sort_hist<<<nchunks, 1024, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
@@ -1084,6 +1153,8 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
         k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(
             ids, static_cast<int>(T), k, E, w.rank, w.hist, w.offsets, tiles ? gemv_max : 0x7FFFFFFF, w.sorted,
             w.pair_pos);
+        if (fork)
+            k_fork_store<<<1, 64, 0, s>>>(w.sync + kForkDone, 0u, withhold ? nullptr : w.sync + kForkSorted, 1u);
     }
     return launch_status();
 }
@@ -1225,8 +1296,12 @@ const char* wl_error_string(int code) {
         case WL_EINVAL_COUNT: return "expert count must be in 1..64";
         case WL_EINVAL_OVERLAP: return "y overlaps x: the layer writes y while x is still being read";
         case WL_ESYNC:
-            return "a fused-kernel workgroup gave up waiting for another (not every workgroup was resident): the "
-                   "outputs of the calls since the last status query hold NaN";
+            return "a bounded wait gave up: a fused-kernel workgroup waiting for another (not every workgroup was "
+                   "resident; those outputs hold NaN) or a fork-scope hand-off (the scope's MFMA experts were "
+                   "skipped since; those outputs are stale)";
+        case WL_EINVAL_SCOPE:
+            return "fork scope: wl_moe_fork_begin with a scope already open on this device, or wl_moe_fork_end "
+                   "without one open on this stream";
         case WL_EINVAL_SCRATCH:
             return "the call needs more workspace than wl_moe_layer_noalloc's scratch holds "
                    "(WL_NOALLOC_SCRATCH_BYTES): use wl_moe_layer with a workspace";
@@ -1270,17 +1345,24 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
 // per layer against the GEMV experts there). The stream and events are created on a device's first split call and
 // kept; the whole fork-to-join sequence runs under one lock, so concurrent calls from several host threads stay
 // correct (their MFMA work queues on the one second stream). Under graph capture the fork and join become graph
-// edges.
+// edges. A fork scope (wl_moe_fork_begin / wl_moe_fork_end) forks and joins once for many calls on one stream, and
+// the calls inside it hand their MFMA work over through workspace words (k_fork_wait, k_fork_store): two graph
+// edges for a 40-layer step instead of two per layer, each pair costing ~10 us of the layer.
 struct ForkStreams {
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    bool scope_open = false;
+    hipStream_t scope = nullptr;  // the open scope's stream
 };
 constexpr int kForkDevices = 64;
 static ForkStreams g_fork[kForkDevices];
 static std::mutex g_fork_lock;
+// fork-scope waits: polls (each after a short sleep) before giving up; WL_MOE_TEST_STARVE: the grouping does not
+// publish itself and the second stream's wait gives up after kForkStarveSpin
+constexpr uint32_t kForkSpin = 1u << 22, kForkStarveSpin = 1u << 11;
 
 // This device's fork resources (created on first use), or nullptr with *rc set.
-static const ForkStreams* fork_streams(int* rc) {
+static ForkStreams* fork_streams(int* rc) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= kForkDevices) {
@@ -1352,6 +1434,25 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     const ExpertPlan plan = expert_plan(L, tokens);
     const bool mfma = plan != kPlanGemv;
     const int gemv_max = plan_gemv_max(plan);
+    // routed experts that may run on the GEMV kernels: each holds between 1 and gemv_max pairs
+    const int64_t P = tokens * L.top_k;
+    // the second stream is worth it while the experts average fewer than kForkMaxAvg tokens (at prefill sizes nearly
+    // every expert is an MFMA expert, and the second stream's empty GEMV launches cost more than they overlap: 22.4
+    // -> 22.7 ms per 4096-token chunk)
+    constexpr int64_t kForkMaxAvg = 32;
+    const bool few_gemv = plan == kPlanSplit && P >= kForkMaxAvg * L.n_experts;
+    // with a split plan (and no stage events) the MFMA experts run on the device's second stream, in an open fork
+    // scope on this stream handed over through the workspace's fork words, else forked and joined by events
+    ForkStreams* fk = nullptr;
+    bool in_scope = false;
+    std::unique_lock<std::mutex> fork_guard;
+    if (plan == kPlanSplit && may_fork && !events && !few_gemv) {
+        fork_guard = std::unique_lock<std::mutex>(g_fork_lock);
+        fk = fork_streams(&rc);
+        if (!fk) return rc;
+        in_scope = fk->scope_open && fk->scope == s;
+    }
+    const bool starve = (L.flags & WL_MOE_TEST_STARVE) != 0;
     rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s)
                                          : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
     if (rc) return rc;
@@ -1359,38 +1460,30 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
     if (rc) return rc;
     mark(2);
-    rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, s);
+    rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, in_scope, starve, s);
     if (rc) return rc;
     mark(3);
-    // routed experts that may run on the GEMV kernels: each holds between 1 and gemv_max pairs
-    const int64_t P = tokens * L.top_k;
     const int max_gemv = plan == kPlanMfma ? 0 : static_cast<int>(P < L.n_experts ? P : L.n_experts);
     // the shared expert runs on the MFMA GEMMs in an MFMA plan (it sees every token), else on the GEMV kernels
     const ExpertArgs ga = gemv_args(L, x, tokens, w, max_gemv, shared && !mfma);
-    // the MFMA experts' stream: the caller's, or with a split plan (and no stage events) the device's second stream
-    hipStream_t s_mfma = s;
-    const ForkStreams* fk = nullptr;
-    std::unique_lock<std::mutex> fork_guard;
-    // worth it while the experts average fewer than kForkMaxAvg tokens (at prefill sizes nearly every expert is an
-    // MFMA expert, and the second stream's empty GEMV launches cost more than they overlap: 22.4 -> 22.7 ms per
-    // 4096-token chunk)
-    constexpr int64_t kForkMaxAvg = 32;
-    const bool few_gemv = plan == kPlanSplit && P >= kForkMaxAvg * L.n_experts;
     // the GEMV launches' grid bound: at prefill sizes a GEMV expert is rare, and a grid sized for one per possible
     // expert costs ~4.5 us per launch to dispatch and retire empty; one workgroup per CU loops over whatever items
     // there are
     const int gemv_slots = few_gemv && max_gemv > 8 ? 8 : max_gemv;
-    if (plan == kPlanSplit && may_fork && !events && !few_gemv) {
-        fk = fork_streams(&rc);
-        if (!fk) return rc;
-        fork_guard = std::unique_lock<std::mutex>(g_fork_lock);
-        hipError_t e = hipEventRecord(fk->fork, s);
-        if (e == hipSuccess) e = hipStreamWaitEvent(fk->side, fk->fork, 0);
-        if (e != hipSuccess) return static_cast<int>(e);
+    hipStream_t s_mfma = s;  // the MFMA experts' stream
+    const uint32_t* skip = in_scope ? w.sync + kForkSkip : nullptr;
+    if (fk) {
         s_mfma = fk->side;
+        if (in_scope) {
+            k_fork_wait<<<1, 64, 0, s_mfma>>>(w.sync, starve ? kForkStarveSpin : kForkSpin);
+        } else {
+            hipError_t e = hipEventRecord(fk->fork, s);
+            if (e == hipSuccess) e = hipStreamWaitEvent(s_mfma, fk->fork, 0);
+            if (e != hipSuccess) return static_cast<int>(e);
+        }
     }
     if (mfma) {
-        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, plan == kPlanSplit, s_mfma);
+        rc = launch_mfma_gate_up(L, tokens, w, gemv_max, plan == kPlanSplit, skip, s_mfma);
         if (rc) return rc;
     }
     launch_gemv_gate_up(L, ga, gemv_slots, shared && !mfma, s);
@@ -1398,28 +1491,34 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     if (rc) return rc;
     mark(4);
     if (mfma) {
-        rc = launch_mfma_down(L, tokens, w, gemv_max, s_mfma);
+        rc = launch_mfma_down(L, tokens, w, gemv_max, skip, s_mfma);
         if (rc) return rc;
     }
     launch_gemv_down(L, ga, gemv_slots, shared && !mfma, s);
     rc = launch_status();
     if (rc) return rc;
-    if (fk) {  // join: the combine waits for the MFMA experts
+    if (in_scope) {  // the combine waits for kForkDone
+        k_fork_store<<<1, 64, 0, s_mfma>>>(nullptr, 0u, w.sync + kForkDone, 1u);
+        rc = launch_status();
+        if (rc) return rc;
+    } else if (fk) {  // join: the combine waits for the MFMA experts
         hipError_t e = hipEventRecord(fk->join, s_mfma);
         if (e == hipSuccess) e = hipStreamWaitEvent(s, fk->join, 0);
         if (e != hipSuccess) return static_cast<int>(e);
-        fork_guard.unlock();
     }
+    if (fork_guard.owns_lock()) fork_guard.unlock();
+    uint32_t* combine_wait = in_scope ? w.sync : nullptr;
     mark(5);
     const unsigned cgrid = static_cast<unsigned>(tokens * ((L.hidden + kCombineSpan - 1) / kCombineSpan));
     if (mfma)
         k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
                                                   w.wts, w.o,
                                                   shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg,
-                                                  resid, y);
+                                                  resid, y, combine_wait, kForkSpin);
     else
         k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y);
+                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y, combine_wait,
+                                               kForkSpin);
     rc = launch_status();
     mark(6);
     return rc;
@@ -1429,6 +1528,36 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
 int wl_moe_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids, float* weights,
                  void* workspace, size_t workspace_bytes, void* stream) {
     return run_layer(layer, x, tokens, y, ids, weights, workspace, workspace_bytes, stream, nullptr, true);
+}
+
+int wl_moe_fork_begin(void* stream) {
+    std::lock_guard<std::mutex> guard(g_fork_lock);
+    int rc = WL_OK;
+    ForkStreams* fk = fork_streams(&rc);
+    if (!fk) return rc;
+    if (fk->scope_open) return WL_EINVAL_SCOPE;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipEventRecord(fk->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(fk->side, fk->fork, 0);
+    if (e != hipSuccess) return static_cast<int>(e);
+    fk->scope_open = true;
+    fk->scope = s;
+    return WL_OK;
+}
+
+int wl_moe_fork_end(void* stream) {
+    std::lock_guard<std::mutex> guard(g_fork_lock);
+    int rc = WL_OK;
+    ForkStreams* fk = fork_streams(&rc);
+    if (!fk) return rc;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!fk->scope_open || fk->scope != s) return WL_EINVAL_SCOPE;
+    hipError_t e = hipEventRecord(fk->join, fk->side);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, fk->join, 0);
+    if (e != hipSuccess) return static_cast<int>(e);
+    fk->scope_open = false;
+    fk->scope = nullptr;
+    return WL_OK;
 }
 
 int wl_moe_layer_profile(const WlMoeLayer* layer, const float* x, int64_t tokens, float* y, int32_t* ids,
@@ -1530,6 +1659,15 @@ extern "C" int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, 
     e = hipMemcpy(&v, word, sizeof(v), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return static_cast<int>(e);
     if (!v) return WL_OK;
+    if (v & kStatusFork) {  // a fork-scope wait gave up: once the second stream has drained, its words start over
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) return static_cast<int>(e);
+        uint32_t* base = static_cast<uint32_t*>(ws);
+        for (const int i : {kForkSorted, kForkDone, kForkSkip}) {
+            const int rz = zero_words(base + i, 1, s);
+            if (rz) return rz;
+        }
+    }
     int rc = zero_words(word, 1, s);
     if (rc) return rc;
     e = hipStreamSynchronize(s);

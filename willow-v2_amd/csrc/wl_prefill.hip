@@ -713,6 +713,7 @@ __device__ __forceinline__ void slab_tile(int nslab, int& slab, int& tile) {
 template <int TYPE, int TILE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<TILE>()];
+    if (a.skip && *a.skip) return;
     int slab, ti;
     slab_tile(a.nslab_gate_up, slab, ti);
     const int4* tiles = TILE == kTileTokens ? a.tiles : a.tiles_down;
@@ -761,6 +762,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up(PrefillArgs a) {
 template <int TYPE>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t bufs[2][tile_bytes<kDownTileTokens>()];
+    if (a.skip && *a.skip) return;
     int group, ti;
     slab_tile(a.H / 256 / a.down_slabs, group, ti);
     int4 tile;
@@ -922,6 +924,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_gate_up_ks(PrefillArgs a)
     __shared__ __attribute__((aligned(16))) uint8_t lds[KQ * kKsTile * kTileRowBytes];
     static_assert(kRT == 2, "one gate and one up row tile per wavefront");
     constexpr int kSlab = 16 * kGemmWaves / KQ;
+    if (a.skip && *a.skip) return;
     int slab, ti;
     slab_tile(a.nslab_gate_up, slab, ti);
     if (ti >= a.n_tiles[0]) return;
@@ -959,6 +962,7 @@ template <int TYPE, int KQ>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm_down_ks(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[KQ * kKsTile * kTileRowBytes];
     constexpr int kRows = 16 * kRT * kGemmWaves / KQ;
+    if (a.skip && *a.skip) return;
     int group, ti;
     slab_tile(a.H / kRows, group, ti);
     if (ti >= a.n_tiles_down[0]) return;
@@ -1109,8 +1113,9 @@ static int launch_gate_up_ks(const WlMoeLayer& L, int64_t T, PrefillArgs a, int 
 // The MFMA experts' gate_up + SwiGLU (the routed experts with more than gemv_max pairs and the shared expert).
 // The routed and shared experts share one launch, so their types must agree (checked by prefill_eligible).
 int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, bool with_gemv,
-                        hipStream_t s) {
+                        const uint32_t* skip, hipStream_t s) {
     PrefillArgs a = prefill_args(L, T, w);
+    a.skip = skip;
     if (ks_eligible(L, T))
         return with_gemv ? launch_gate_up_ks<kKsGateUpBeside>(L, T, a, gemv_max, s)
                          : launch_gate_up_ks<kKsGateUp>(L, T, a, gemv_max, s);
@@ -1126,8 +1131,10 @@ int launch_mfma_gate_up(const WlMoeLayer& L, int64_t T, const Workspace& w, int 
 }
 
 // The MFMA experts' down products.
-int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, hipStream_t s) {
-    const PrefillArgs a = prefill_args(L, T, w);
+int launch_mfma_down(const WlMoeLayer& L, int64_t T, const Workspace& w, int gemv_max, const uint32_t* skip,
+                     hipStream_t s) {
+    PrefillArgs a = prefill_args(L, T, w);
+    a.skip = skip;
     if (ks_eligible(L, T)) {
         const dim3 grid(static_cast<unsigned>(L.hidden / kKsRows * tiles8(L, T, kDownTileTokens, gemv_max)));
         if (L.down_type == WL_TYPE_Q4_K)

@@ -21,7 +21,8 @@ MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many 
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA, MOE_TEST_STARVE, MOE_PRE_NORM, MOE_RESIDUAL = 1, 2, 4, 8, 16, 32
-ESYNC = -10  # wl_moe_workspace_status: a fused-kernel wait gave up
+ESYNC = -10  # wl_moe_workspace_status: a bounded wait gave up
+EINVAL_SCOPE = -12  # wl_moe_fork_begin / wl_moe_fork_end used outside their pairing
 NOALLOC_SCRATCH_BYTES = 16 << 20  # WL_NOALLOC_SCRATCH_BYTES
 
 LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwillow_hip.so")
@@ -85,6 +86,8 @@ def library() -> ctypes.CDLL:
     lib.wl_moe_stage_name.argtypes, lib.wl_moe_stage_name.restype = [c_int], ctypes.c_char_p
     lib.wl_moe_layer_noalloc.argtypes, lib.wl_moe_layer_noalloc.restype = [layer_p, vp, i64, vp, vp, vp, vp], c_int
     lib.wl_moe_workspace_status.argtypes, lib.wl_moe_workspace_status.restype = [vp, ctypes.c_size_t, vp], c_int
+    lib.wl_moe_fork_begin.argtypes, lib.wl_moe_fork_begin.restype = [vp], c_int
+    lib.wl_moe_fork_end.argtypes, lib.wl_moe_fork_end.restype = [vp], c_int
     for name in ("wl_dequant", "wl_gemv", "wl_linear", "wl_gemv_batch", "wl_gemv_combine", "wl_moe_check", "wl_moe_route",
                  "wl_moe_layer", "wl_moe_layer_profile"):
         getattr(lib, name).restype = c_int
@@ -127,6 +130,26 @@ def _type_id(type_name: str) -> int:
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class fork_scope:
+    """A fork scope on the current stream of `device` (wl_moe_fork_begin / wl_moe_fork_end): the split-plan layer
+    calls inside it hand their MFMA experts to the device's second stream through their workspaces instead of a
+    fork and a join event each (under graph capture, two graph edges for the whole block instead of two per call).
+    Use it around a block of layer calls issued in order from one thread, e.g. the layers of one decode step."""
+
+    def __init__(self, device=None):
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.stream = None
+
+    def __enter__(self):
+        self.stream = _stream(self.device)
+        check(library().wl_moe_fork_begin(self.stream))
+        return self
+
+    def __exit__(self, *exc):
+        check(library().wl_moe_fork_end(self.stream))
+        return False
 
 
 def _on_gpu(t: torch.Tensor, what: str):

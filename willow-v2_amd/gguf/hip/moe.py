@@ -191,8 +191,8 @@ class MoELayer:
 
     def status(self, workspace: torch.Tensor = None) -> int:
         """wl_moe_workspace_status on `workspace` (default: this layer's own). Synchronizes the stream; returns 0,
-        or -10 (ESYNC) when a fused-kernel wait gave up since the previous query (the outputs of those calls hold
-        NaN)."""
+        or -10 (ESYNC) when a bounded wait gave up since the previous query (a fused-kernel wait: those outputs
+        hold NaN; a fork-scope hand-off: the scope's MFMA experts were skipped since)."""
         ws = workspace if workspace is not None else self._ws
         if ws is None:
             return 0
