@@ -2,10 +2,13 @@
 the library's second stream and back through words of their workspace instead of a fork and a join event each.
 They run the same kernels in the same order of arithmetic, so every result equals the same call outside a scope bit
 for bit: eagerly, captured in a graph and replayed with eager work in between, with one workspace shared by the
-layers or one each, and on the full-shape Zipf batched-decode layer. Misuse of the scope is an error, and a
+layers or one each, at prefill sizes (where a call takes no second stream), on the full-shape Zipf batched-decode
+layer, and through a chained decoder step (pre-norm and residual, each layer reading the previous one's output). Misuse of the scope is an error, and a
 hand-off that gives up (forced from the host: the grouping withholds its flag, the wait gives up after a short
 bounded spin and the MFMA kernels are skipped, so every kernel exits) is reported once by wl_moe_workspace_status,
 after which the next call is correct again."""
+import contextlib
+
 import pytest
 import torch
 
@@ -76,6 +79,36 @@ def test_scope_graph_replays_match_eager(layers):
     assert layers[0].status(ws) == 0
 
 
+@pytest.mark.parametrize("graph", [False, True])
+def test_scope_prefill_size_matches_per_call(layers, graph):
+    """At prefill sizes (experts averaging 32 tokens or more) a split call takes no second stream, in a scope or
+    not: the same results, eagerly and replayed."""
+    tokens = 300
+    ws = new_workspace(max(layer.workspace_bytes(tokens) for layer in layers), "cuda")
+    xs = inputs(1100, tokens=tokens)
+    want = per_call(layers, xs)
+    y = torch.zeros_like(want)
+
+    def step():
+        with hip.fork_scope():
+            for l, layer in enumerate(layers):
+                layer(xs[l], out=y[l], workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(y, want), f"max diff {(y - want).abs().max().item()}"
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=torch.cuda.Stream()):
+            step()
+        for rep in range(3):
+            y.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, want), f"replay {rep}: max diff {(y - want).abs().max().item()}"
+    assert layers[0].status(ws) == 0
+
+
 def test_scope_zipf_b64_matches_per_call():
     """The batched-decode workload's layer (256 experts, Zipf(1.1) routing, 64 tokens), as the benchmark runs it."""
     layer = MoELayer.from_host(synth.moe_layer(3, zipf_alpha=1.1))
@@ -88,6 +121,29 @@ def test_scope_zipf_b64_matches_per_call():
     torch.cuda.synchronize()
     assert torch.equal(got, want), f"max diff {(got - want).abs().max().item()}"
     assert layer.status(ws) == 0
+
+
+def test_scope_chained_decoder_step(layers):
+    """A decoder step's MoE half chained through the layers, x <- x + MoE(rms_norm(x)) (WL_MOE_PRE_NORM and
+    WL_MOE_RESIDUAL, each layer reading the previous one's output), in one scope and per call: the same bits."""
+    chained = [layer.with_norm(torch.from_numpy(synth.tokens(40 + l, 1)[0] * 0.1).cuda()) for l, layer in
+               enumerate(layers)]
+    ws = new_workspace(max(layer.workspace_bytes(TOKENS) for layer in chained), "cuda")
+    x0 = inputs(1300, n=1)[0]
+
+    def run(scoped):
+        xs = [x0]
+        with hip.fork_scope() if scoped else contextlib.nullcontext():
+            for layer in chained:
+                xs.append(layer(xs[-1], workspace=ws))
+        torch.cuda.synchronize()
+        return torch.stack(xs[1:])
+
+    want = run(False)
+    got = run(True)
+    assert torch.isfinite(want).all()
+    assert torch.equal(got, want), f"max diff {(got - want).abs().max().item()}"
+    assert chained[0].status(ws) == 0
 
 
 def test_scope_misuse_is_an_error():
