@@ -146,6 +146,32 @@ def test_layer_multi_chunk_sort(hip, c2, layer_c2):
     check_layer(hip, c2, layer_c2, synth.tokens(300, 300), "c2 T=300")
 
 
+@pytest.mark.parametrize("case", ["c2", "zipf_bias", "no_shared_gate", "experts_40"])
+def test_layer_routing_equals_route(hip, layer_c2, case):
+    """wl_moe_layer routes 2 to 64 tokens with the K-split router (k_router_parts: per-segment partials from 4x the
+    workgroups, added in segment order by k_topk_parts); its ids and routing weights equal wl_moe_route's (the
+    one-kernel router, then k_topk) bit for bit, so the logits are the same bits: at 1 and 65 tokens, either side of
+    its range, too."""
+    if case == "c2":
+        lw = layer_c2
+    elif case == "zipf_bias":  # a router bias (log-Zipf)
+        lw = synth.moe_layer(3, zipf_alpha=1.1)
+    elif case == "no_shared_gate":
+        lw = dict(synth.moe_layer(7, experts=64, top_k=8))
+        lw["shared_gate"] = None
+    else:  # rows not a multiple of 16
+        lw = synth.moe_layer(8, experts=40, top_k=4)
+    layer = hip.MoELayer.from_host(lw)
+    for T in (1, 2, 9, 33, 64, 65):
+        x = synth.tokens(60 + T, T)
+        _, ids, wts = run_layer(hip, layer, x)
+        w_ref, ids_ref, _ = layer.route(torch.from_numpy(x).cuda())
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ids, ids_ref.cpu().numpy(), err_msg=f"{case} T={T}")
+        np.testing.assert_array_equal(wts.view(np.uint32), w_ref.cpu().numpy().view(np.uint32),
+                                      err_msg=f"{case} T={T}")
+
+
 def test_layer_zipf_b64(hip):
     """The batched-decode case: 64 tokens, expert popularity Zipf(1.1)-shaped through a router bias."""
     lw = synth.moe_layer(3, zipf_alpha=1.1)

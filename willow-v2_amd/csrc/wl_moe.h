@@ -71,6 +71,7 @@ constexpr int kDownSlabsMax = 4;            // prefill: most 256-row slabs per d
 constexpr int kGemvMaxTokens = 8;
 constexpr uint32_t kPosBf16 = 0x80000000u;  // pair_pos flag: the pair's expert output is bf16 (an MFMA expert)
 constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
+constexpr int kRouterPartsMaxT = 64;         // wl_moe_layer's router for 2 .. this many tokens: per-segment partials
 
 struct PrefillArgs {
     const uint8_t* gate_up;
@@ -122,6 +123,7 @@ struct Workspace {
     uint16_t* h16;      // [T*k, inter] bf16
     uint16_t* h_sh16;   // [T, shared_inter] bf16
     float* xn;          // [T, hidden] the normalized input (WL_MOE_PRE_NORM)
+    float* parts;       // [hidden / kRouterSeg, T, E + 1] the router's segment partials (2 .. kRouterPartsMaxT tokens)
     size_t bytes;
 };
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "wl_common.h"
 #include "wl_host.h"
@@ -181,6 +182,121 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, 
     if (lane < k) {
         ids[static_cast<int64_t>(t) * k + lane] = id;
         wts[static_cast<int64_t>(t) * k + lane] = w;
+        if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Router for a few tokens (2 .. kRouterPartsMaxT, inside wl_moe_layer), the K loop spread over 4x the workgroups of
+// k_router_split: a workgroup takes 16 tokens x 16 rows and kRsWaves consecutive segments, its wavefront w the
+// segment kRsWaves blockIdx.z + w, whose partial (the 64-value fused multiply-add chain from zero, on the fp32
+// matrix core, staged as in k_router_split) it stores to parts[seg][t][r], rows r < E + (shared gate); no barrier
+// and no partial sum inside the workgroup. k_topk_parts then adds each row's partials in segment order and the
+// bias: the order of router_row, so the logits are the same bits. With xb, the first row tile's workgroups also
+// store the tokens' values as bf16.
+__global__ __launch_bounds__(64 * kRsWaves) void k_router_parts(const float* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ shared_gate, int T,
+                                                                int H, int E, float* __restrict__ parts,
+                                                                uint16_t* __restrict__ xb) {
+    __shared__ __attribute__((aligned(16))) float stage[kRsWaves][2][kRsTile];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+    const int rows = E + (shared_gate ? 1 : 0);
+    const int seg = static_cast<int>(blockIdx.z) * kRsWaves + wv;
+    if (seg >= H / kRouterSeg) return;  // the wavefront alone: nothing below synchronizes the workgroup
+    // float4 f = lane + 64 i (i < 4) holds values 4 (f % 16) .. + 3 of the segment for token / row f / 16
+    float4 xn[4], wn[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int f = lane + 64 * i, rr = f >> 4, c4 = 4 * (f & 15);
+        const int t = t0 + rr, r = r0 + rr;
+        xn[i] = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(t < T ? t : T - 1) * H + seg * kRouterSeg +
+                                                 c4);
+        const float* wr = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) : nullptr;
+        wn[i] = wr ? *reinterpret_cast<const float4*>(wr + seg * kRouterSeg + c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float* sa = stage[wv][0];
+    float* sb = stage[wv][1];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int f = lane + 64 * i, rr = f >> 4, s4 = f & 15;
+        const float4 xv = xn[i], wv4 = wn[i];
+        if (xb && blockIdx.y == 0 && t0 + rr < T)
+            *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + seg * kRouterSeg + 4 * s4) =
+                make_uint2(pack2(xv.x, xv.y), pack2(xv.z, xv.w));
+        sa[(0 * 16 + rr) * kRsRow + s4] = xv.x;
+        sa[(1 * 16 + rr) * kRsRow + s4] = xv.y;
+        sa[(2 * 16 + rr) * kRsRow + s4] = xv.z;
+        sa[(3 * 16 + rr) * kRsRow + s4] = xv.w;
+        sb[(0 * 16 + rr) * kRsRow + s4] = wv4.x;
+        sb[(1 * 16 + rr) * kRsRow + s4] = wv4.y;
+        sb[(2 * 16 + rr) * kRsRow + s4] = wv4.z;
+        sb[(3 * 16 + rr) * kRsRow + s4] = wv4.w;
+    }
+    lane_sync();
+    const int lt = lane & 15, lj = lane >> 4;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    floatx4 acc;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // steps s = 4 q .. 4 q + 3
+        const float4 av = *reinterpret_cast<const float4*>(&sa[(lj * 16 + lt) * kRsRow + 4 * q]);
+        const float4 bv = *reinterpret_cast<const float4*>(&sb[(lj * 16 + lt) * kRsRow + 4 * q]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, q == 0 ? zero : acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+    }
+    // lane holds D[4 lj + i][lt]: token t0 + 4 lj + i, row r0 + lt
+    const int r = r0 + lt;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = t0 + 4 * lj + i;
+        if (t < T && r < rows) parts[(static_cast<int64_t>(seg) * T + t) * rows + r] = acc[i];
+    }
+}
+
+// Top-k over k_router_parts' partials: one workgroup per token. Thread r adds row r's nseg partials in segment
+// order (then the bias; the shared gate's row E gives sg[t] = sigmoid of its sum) into LDS, with every load of the
+// row issued before the adds when the segment count NSEG is a compile-time one; then wavefront 0 runs wave_topk as
+// k_topk. blockDim.x: rows rounded up to a wavefront, at most 1024 (beyond, threads take several rows).
+template <int EJ, int NSEG>
+__global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ parts, int nseg,
+                                                     const float* __restrict__ bias, int T, int E, int rows, int k,
+                                                     int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                     int32_t* __restrict__ corder, float* __restrict__ sg) {
+    __shared__ float lg[64 * EJ];
+    __shared__ uint32_t scratch[64];
+    const int t = blockIdx.x;
+    const int64_t stride = static_cast<int64_t>(T) * rows;
+    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+        const float* p = parts + static_cast<int64_t>(t) * rows + r;
+        float tot;
+        if constexpr (NSEG > 0) {
+            float v[NSEG];
+#pragma unroll
+            for (int i = 0; i < NSEG; i++) v[i] = p[i * stride];
+            tot = v[0];
+#pragma unroll
+            for (int i = 1; i < NSEG; i++) tot = __fadd_rn(tot, v[i]);
+        } else {
+            tot = p[0];
+            for (int i = 1; i < nseg; i++) tot = __fadd_rn(tot, p[i * stride]);
+        }
+        if (r < E)
+            lg[r] = bias ? __fadd_rn(tot, bias[r]) : tot;
+        else
+            sg[t] = sigmoid(tot);
+    }
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    int id, id_rank;
+    float wsel;
+    wave_topk<EJ>(lg, E, k, renorm != 0, scratch, lane, id, wsel, id_rank);
+    if (lane < k) {
+        ids[static_cast<int64_t>(t) * k + lane] = id;
+        wts[static_cast<int64_t>(t) * k + lane] = wsel;
         if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
     }
 }
@@ -1022,6 +1138,9 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Carves the workspace; with base == nullptr only computes the size.
+// Whether wl_moe_layer's router runs as k_router_parts + k_topk_parts (a single token runs the fused kernel).
+static bool router_parts(int64_t T) { return T >= 2 && T <= kRouterPartsMaxT; }
+
 Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     Workspace w{};
     const int64_t P = T * L.top_k;
@@ -1059,6 +1178,8 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.h16 = static_cast<uint16_t*>(take(mfma ? sizeof(uint16_t) * P * L.inter : 0));
     w.h_sh16 = static_cast<uint16_t*>(take(mfma && shared ? sizeof(uint16_t) * T * L.shared_inter : 0));
     w.xn = static_cast<float*>(take((L.flags & WL_MOE_PRE_NORM) ? sizeof(float) * T * L.hidden : 0));
+    w.parts = static_cast<float*>(take(router_parts(T) ? sizeof(float) * (L.hidden / kRouterSeg) * T *
+                                                             (L.n_experts + 1) : 0));
     w.bytes = off;
     return w;
 }
@@ -1131,6 +1252,37 @@ static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int3
         k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
     else
         k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+    return launch_status();
+}
+
+// Router and top-k of a call of 2 .. kRouterPartsMaxT tokens: k_router_parts, then k_topk_parts.
+static int launch_router_parts(const WlMoeLayer& L, const float* x, int64_t T, const Workspace& w, uint16_t* xb,
+                               hipStream_t s) {
+    const float* shared_gate = (L.shared_gate_up && L.shared_gate) ? L.shared_gate : nullptr;
+    const int rows = L.n_experts + (shared_gate ? 1 : 0);
+    const int nseg = L.hidden / kRouterSeg;
+    k_router_parts<<<dim3(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>((rows + 15) / 16),
+                          static_cast<unsigned>((nseg + kRsWaves - 1) / kRsWaves)),
+                     64 * kRsWaves, 0, s>>>(x, L.router, shared_gate, static_cast<int>(T), L.hidden, L.n_experts,
+                                            w.parts, xb);
+    return launch_status();
+}
+
+static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w, float* sg, hipStream_t s) {
+    const int rows = L.n_experts + ((L.shared_gate_up && L.shared_gate) ? 1 : 0);
+    const int nseg = L.hidden / kRouterSeg;
+    const int Ti = static_cast<int>(T);
+    const unsigned grid = static_cast<unsigned>(T);
+    const int E = L.n_experts, k = L.top_k, rn = L.norm_topk_prob ? 1 : 0;
+    const unsigned threads = static_cast<unsigned>(rows + 63) / 64 * 64 < 1024u ? (rows + 63) / 64 * 64 : 1024u;
+    // every instance has the same parameters; 32 segments: hidden 2048
+    auto pick = [&](auto seg32) {
+        constexpr int S = decltype(seg32)::value;
+        return E <= 64 ? k_topk_parts<1, S> : E <= 128 ? k_topk_parts<2, S> : E <= 256 ? k_topk_parts<4, S>
+               : E <= 512 ? k_topk_parts<8, S> : k_topk_parts<16, S>;
+    };
+    auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
+    kernel<<<grid, threads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts, w.corder, sg);
     return launch_status();
 }
 
@@ -1453,13 +1605,23 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         in_scope = fk->scope_open && fk->scope == s;
     }
     const bool starve = (L.flags & WL_MOE_TEST_STARVE) != 0;
-    rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s)
-                                         : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
-    if (rc) return rc;
-    mark(1);
-    rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
-    if (rc) return rc;
-    mark(2);
+    if (router_parts(tokens)) {
+        rc = launch_router_parts(L, x, tokens, w, mfma ? w.xb : nullptr, s);
+        if (rc) return rc;
+        mark(1);
+        rc = launch_topk_parts(L, tokens, w, sg, s);
+        if (rc) return rc;
+        mark(2);
+    } else {
+        rc = tokens >= kTiledRouterMinTokens
+                 ? launch_router_tiled(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s)
+                 : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
+        if (rc) return rc;
+        mark(1);
+        rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
+        if (rc) return rc;
+        mark(2);
+    }
     rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, in_scope, starve, s);
     if (rc) return rc;
     mark(3);
