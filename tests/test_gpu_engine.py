@@ -1,5 +1,7 @@
 """The drop-in: Engine.moe through the HipMoE mixin on an HBM-resident expert store, against the CPU oracle, with
 the engine attributes and weight names the reference's Engine uses (engines/base.py:285-286,445-490)."""
+import contextlib
+
 import numpy as np
 import pytest
 import torch
@@ -94,7 +96,7 @@ def rms_norm_zero_centered(x, w, eps=1e-6):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * (1 + w)
 
 
-@pytest.mark.parametrize("tokens", [1, 9])
+@pytest.mark.parametrize("tokens", [1, 9, 40])  # 40: experts of more than 8 tokens, the second stream
 def test_engine_model_loop(tokens):
     """The MoE half of the decoder loop as engines/qwen36/model.py:22 runs it, x = x + moe(rms_norm(x), layer,
     residual=x), over three layers of one HBMExpertStore through HipMoE.moe: each layer names the next (the
@@ -120,3 +122,14 @@ def test_engine_model_loop(tokens):
     assert sorted(views) == [0, 1, 2]
     assert views[0][0]._next is views[1][0] and views[1][0]._next is views[2][0]
     assert torch.isfinite(x).all()
+    # the same loop as one decode step in the engine's fork scope: the same bits
+    x1 = torch.from_numpy(synth.tokens(91 + tokens, tokens)).cuda()
+    outs = []
+    for scoped in (False, True):
+        xs = x1
+        with eng.moe_step() if scoped else contextlib.nullcontext():
+            for l in range(len(lws)):
+                xs = xs + eng.moe(rms_norm_zero_centered(xs, norm_w[l]), l, residual=xs)
+        torch.cuda.synchronize()
+        outs.append(xs)
+    assert torch.equal(outs[0], outs[1])

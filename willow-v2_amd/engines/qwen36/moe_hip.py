@@ -14,6 +14,11 @@ launches. In place of guess_next_layer (engines/base.py:392-406), which guesses 
 their SSD reads, each layer's view names the next layer, and a batch-1 call pulls the next layer's router and
 shared-expert rows (read before its routing is known) into the GPU's caches while it waits on its own exchanges.
 
+Batched decode: a runner may wrap one decode step's layers (attention included) in `with engine.moe_step():`, a
+fork scope of the library (gguf.hip.fork_scope): the layers' experts given more than 8 tokens then meet the rest
+through the workspace instead of a fork and a join per layer (64 tokens, Zipf routing: ~10 us per layer). The
+step's calls must come from one thread, in order, on the current stream.
+
 Shared expert: when its three matrices are GGMLWeight (kept quantized), they run inside the fused kernel; when
 they are dense tensors (the reference's loader dequantizes them to bf16, engines/qwen36/loader.py:224), the
 routed part runs fused and the shared expert is added with the reference's own formula (engines/base.py:104-107).
@@ -22,7 +27,7 @@ Arithmetic is fp32 inside the kernel; the result is cast back to x's dtype.
 import torch
 import torch.nn.functional as F
 
-from gguf.hip import GGMLWeight
+from gguf.hip import GGMLWeight, fork_scope
 
 
 def dense_shared_expert(x, gate_w, up_w, down_w, shared_gate_w):
@@ -68,6 +73,10 @@ class HipMoE:
         view = self.experts.layer_view(layer, router, self.top_k, self.norm_topk_prob, router_bias=bias, **shared)
         cache[layer] = (view, dense)
         return cache[layer]
+
+    def moe_step(self):
+        """A context for one decode step's layers: the library's fork scope on the experts' device."""
+        return fork_scope(self.experts.device)
 
     def moe(self, x: torch.Tensor, layer: int, residual: torch.Tensor = None) -> torch.Tensor:
         view, dense = self.hip_layer(layer)
