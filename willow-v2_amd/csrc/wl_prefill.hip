@@ -55,8 +55,9 @@ __device__ __forceinline__ uint2 load8_a2(const uint8_t* p) {
 // the TM x 2 tiles of 16 x 16 at tokens 16 TM (w & 1) + 16 m and rows 32 (w >> 1) + 16 n. Per segment the operands
 // are staged in LDS as [j][token or row][s] with 20-float rows: lane (l % 16, j = l / 16) reads its 16 values of the
 // segment as four 16-byte loads, and the 8 lanes of one LDS cycle fall in 8 different bank groups. The staging is
-// double-buffered: while segment s is computed, segment s + 1 is written to the other buffer and segment s + 2 is
-// loaded into registers, one barrier per segment.
+// double-buffered: while segment s is computed, segment s + 1 is written to the other buffer and segment s + 3 is
+// loaded into the register set segment s + 1 leaves (two sets, so each segment's loads have two segments' time to
+// land), one barrier per segment.
 constexpr int kRmRow = 20;
 constexpr int kRouterMfmaTM = 1;  // token tiles of 16 per wavefront
 
@@ -88,13 +89,14 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
         const int r = r0 + ((tid + 256 * q) >> 4);
         wrow[q] = r < rows ? (r < E ? w + static_cast<int64_t>(r) * H : shared_gate) + 4 * s4 : nullptr;
     }
-    float4 xn[kXq], wn[4];
-    auto load_seg = [&](int sgi) {
+    // segment s's loads land in register set s & 1, two segments ahead of its computation
+    float4 xn[2][kXq], wn[2][4];
+    auto load_seg = [&](int sgi, float4 (&xr)[kXq], float4 (&wr)[4]) {
 #pragma unroll
-        for (int q = 0; q < kXq; q++) xn[q] = *reinterpret_cast<const float4*>(xrow[q] + sgi * kRouterSeg);
+        for (int q = 0; q < kXq; q++) xr[q] = *reinterpret_cast<const float4*>(xrow[q] + sgi * kRouterSeg);
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            wn[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + sgi * kRouterSeg)
+            wr[q] = wrow[q] ? *reinterpret_cast<const float4*>(wrow[q] + sgi * kRouterSeg)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     const int lt = lane & 15, lj = lane >> 4;
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
     floatx4 tot[TM][2], acc[TM][2];
     // staging of segment sgi (from registers) into LDS buffer sgi & 1, with x also stored as bf16 once per token
-    auto stage = [&](int sgi) {
+    auto stage = [&](int sgi, const float4 (&xr)[kXq], const float4 (&wr)[4]) {
         float* xsb = xs[sgi & 1];
         float* wsb = ws[sgi & 1];
 #pragma unroll
@@ -110,26 +112,28 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
             const int rr = (tid + 256 * q) >> 4;
             if (xb && blockIdx.y == 0 && t0 + rr < T)  // x as bf16 for the MFMA GEMMs, written once per token
                 *reinterpret_cast<uint2*>(xb + static_cast<int64_t>(t0 + rr) * H + sgi * kRouterSeg + 4 * s4) =
-                    make_uint2(pack2(xn[q].x, xn[q].y), pack2(xn[q].z, xn[q].w));
-            xsb[(0 * kTok + rr) * kRmRow + s4] = xn[q].x;
-            xsb[(1 * kTok + rr) * kRmRow + s4] = xn[q].y;
-            xsb[(2 * kTok + rr) * kRmRow + s4] = xn[q].z;
-            xsb[(3 * kTok + rr) * kRmRow + s4] = xn[q].w;
+                    make_uint2(pack2(xr[q].x, xr[q].y), pack2(xr[q].z, xr[q].w));
+            xsb[(0 * kTok + rr) * kRmRow + s4] = xr[q].x;
+            xsb[(1 * kTok + rr) * kRmRow + s4] = xr[q].y;
+            xsb[(2 * kTok + rr) * kRmRow + s4] = xr[q].z;
+            xsb[(3 * kTok + rr) * kRmRow + s4] = xr[q].w;
         }
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int rr = (tid + 256 * q) >> 4;
-            wsb[(0 * 64 + rr) * kRmRow + s4] = wn[q].x;
-            wsb[(1 * 64 + rr) * kRmRow + s4] = wn[q].y;
-            wsb[(2 * 64 + rr) * kRmRow + s4] = wn[q].z;
-            wsb[(3 * 64 + rr) * kRmRow + s4] = wn[q].w;
+            wsb[(0 * 64 + rr) * kRmRow + s4] = wr[q].x;
+            wsb[(1 * 64 + rr) * kRmRow + s4] = wr[q].y;
+            wsb[(2 * 64 + rr) * kRmRow + s4] = wr[q].z;
+            wsb[(3 * 64 + rr) * kRmRow + s4] = wr[q].w;
         }
     };
-    load_seg(0);
-    stage(0);
-    if (nseg > 1) load_seg(1);
+    load_seg(0, xn[0], wn[0]);
+    if (nseg > 1) load_seg(1, xn[1], wn[1]);
+    stage(0, xn[0], wn[0]);
+    if (nseg > 2) load_seg(2, xn[0], wn[0]);
     __syncthreads();
-    for (int sgi = 0; sgi < nseg; sgi++) {
+    // segment sgi, then segment sgi + 1 staged from its register set (xr, wr) and segment sgi + 3 loaded into it
+    auto segment = [&](int sgi, float4 (&xr)[kXq], float4 (&wr)[4]) {
         const float* xsb = xs[sgi & 1];
         const float* wsb = ws[sgi & 1];
 #pragma unroll
@@ -156,10 +160,10 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
             }
         }
         // the next segment goes into the other buffer, whose last reads (segment sgi - 1) ended before the barrier
-        // that closed the previous iteration; its loads were issued a segment ago
+        // that closed the previous iteration; its loads were issued two segments ago
         if (sgi + 1 < nseg) {
-            stage(sgi + 1);
-            if (sgi + 2 < nseg) load_seg(sgi + 2);
+            stage(sgi + 1, xr, wr);
+            if (sgi + 3 < nseg) load_seg(sgi + 3, xr, wr);
         }
 #pragma unroll
         for (int m = 0; m < TM; m++)
@@ -169,6 +173,10 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
                 for (int i = 0; i < 4; i++)
                     tot[m][n][i] = sgi == 0 ? acc[m][n][i] : __fadd_rn(tot[m][n][i], acc[m][n][i]);
         __syncthreads();  // segment sgi + 1 is staged for everyone; buffer sgi & 1 is free again
+    };
+    for (int sgi = 0; sgi < nseg; sgi += 2) {
+        segment(sgi, xn[1], wn[1]);
+        if (sgi + 1 < nseg) segment(sgi + 1, xn[0], wn[0]);
     }
     // lane holds D[4 lj + i][lt]: token tm0 + 16 m + 4 lj + i, row rn0 + 16 n + lt
 #pragma unroll
