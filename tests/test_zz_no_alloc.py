@@ -1,7 +1,8 @@
 """wl_moe_layer_noalloc (the entry point that allocates nothing: its workspace is a device array inside the
 library) against wl_moe_layer on the same inputs, through the C ABI: outputs and routing bit-identical, on calls
 in a row with shrinking inputs (the scratch keeps the previous call's contents), each plan covered (split MFMA +
-GEMV at 64 tokens, all-GEMV at 5, the fused kernel at 1); a call too large for the scratch is refused."""
+GEMV at 64 tokens, all-GEMV at 5, the fused kernel at 1); a call too large for the scratch is refused; split calls
+inside a fork scope equal the calls outside one."""
 import ctypes
 
 import numpy as np
@@ -46,3 +47,24 @@ def test_noalloc_refuses_oversize(hip, layer_c2):
     assert bool((y == 7.0).all())
     with pytest.raises(ValueError):
         layer.call_noalloc(x, y)
+
+
+def test_noalloc_in_fork_scope(hip):
+    """Split-plan calls of the no-allocation entry point inside a fork scope, three layers in a row: the scratch
+    carries the scope's hand-off words as a shared workspace does, and the results equal the same calls outside a
+    scope bit for bit."""
+    layers = [hip.MoELayer.from_host(synth.moe_layer(190 + i, experts=64, top_k=8)) for i in range(3)]
+    T = 40  # 64 experts, top-8: both expert classes, the second stream used
+    assert all(layer.plan(T) == "split" for layer in layers)
+    xs = [torch.from_numpy(synth.tokens(1500 + i, T)).cuda() for i in range(3)]
+    want = [layer(x) for layer, x in zip(layers, xs)]
+    got = [torch.empty(T, 2048, dtype=torch.float32, device="cuda") for _ in layers]
+    print("[noalloc] fork scope, 3 layers, T=40", flush=True)
+    with hip.fork_scope():
+        for layer, x, y in zip(layers, xs, got):
+            layer.call_noalloc(x, y)
+    torch.cuda.synchronize()
+    assert layers[0].status_noalloc() == 0
+    for i in range(3):
+        assert torch.isfinite(want[i]).all()
+        assert torch.equal(got[i], want[i]), f"layer {i}: max diff {(got[i] - want[i]).abs().max().item()}"
