@@ -39,7 +39,10 @@ constexpr uint32_t kStatusFused = 1u, kStatusFork = 2u;
 constexpr int kForkSorted = kStatusWord + kFlagStride;
 constexpr int kForkDone = kForkSorted + kFlagStride;
 constexpr int kForkSkip = kForkDone + kFlagStride;
-constexpr int kSyncWords = kForkSkip + kFlagStride;
+// and the count of top-k workgroups done in a call of 2 .. kRouterPartsMaxT tokens (the last one runs the grouping
+// and resets it to 0)
+constexpr int kTopkDone = kForkSkip + kFlagStride;
+constexpr int kSyncWords = kTopkDone + kFlagStride;
 
 struct ExpertArgs {
     const uint8_t* gate_up;

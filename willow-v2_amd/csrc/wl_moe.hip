@@ -261,10 +261,10 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_router_parts(const float* __r
 // row issued before the adds when the segment count NSEG is a compile-time one; then wavefront 0 runs wave_topk as
 // k_topk. blockDim.x: rows rounded up to a wavefront, at most 1024 (beyond, threads take several rows).
 template <int EJ, int NSEG>
-__global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ parts, int nseg,
-                                                     const float* __restrict__ bias, int T, int E, int rows, int k,
-                                                     int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                     int32_t* __restrict__ corder, float* __restrict__ sg) {
+__device__ __forceinline__ void topk_parts(const float* __restrict__ parts, int nseg, const float* __restrict__ bias,
+                                           int T, int E, int rows, int k, int renorm, int32_t* __restrict__ ids,
+                                           float* __restrict__ wts, int32_t* __restrict__ corder,
+                                           float* __restrict__ sg) {
     __shared__ float lg[64 * EJ];
     __shared__ uint32_t scratch[64];
     const int t = blockIdx.x;
@@ -289,16 +289,25 @@ __global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ p
             sg[t] = sigmoid(tot);
     }
     __syncthreads();
-    if (threadIdx.x >= 64) return;
-    const int lane = threadIdx.x;
-    int id, id_rank;
-    float wsel;
-    wave_topk<EJ>(lg, E, k, renorm != 0, scratch, lane, id, wsel, id_rank);
-    if (lane < k) {
-        ids[static_cast<int64_t>(t) * k + lane] = id;
-        wts[static_cast<int64_t>(t) * k + lane] = wsel;
-        if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int id, id_rank;
+        float wsel;
+        wave_topk<EJ>(lg, E, k, renorm != 0, scratch, lane, id, wsel, id_rank);
+        if (lane < k) {
+            ids[static_cast<int64_t>(t) * k + lane] = id;
+            wts[static_cast<int64_t>(t) * k + lane] = wsel;
+            if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
+        }
     }
+}
+
+template <int EJ, int NSEG>
+__global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ parts, int nseg,
+                                                     const float* __restrict__ bias, int T, int E, int rows, int k,
+                                                     int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                     int32_t* __restrict__ corder, float* __restrict__ sg) {
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -488,12 +497,10 @@ __global__ __launch_bounds__(64) void k_fork_wait(uint32_t* sync, uint32_t spin_
     __hip_atomic_store(sync + kForkSkip, ok ? 0u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t* __restrict__ ids, int T, int k,
-                                                                  int E, int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ active,
-                                                                  int32_t* __restrict__ sorted,
-                                                                  int32_t* __restrict__ pair_pos, TileOut to,
-                                                                  uint32_t* fork_sync, int withhold) {
+__device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
+                                           int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                           int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos, TileOut to,
+                                           uint32_t* fork_sync, int withhold) {
     __shared__ int32_t lds_ids[kSortChunk * WL_MAX_TOPK];
     __shared__ uint32_t bits[kSortWords * 64 * kMaxEJ];  // expert e: words kSortWords e .. + kSortWords - 1
     __shared__ uint32_t lds_off[64 * kMaxEJ];  // first sorted position | kPosBf16 for an MFMA expert
@@ -537,6 +544,58 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t*
         tile_list(to.tiles_down, to.n_tiles + 1, kDownTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
     }
     if (fork_sync) publish_grouping(fork_sync, withhold);
+}
+
+__global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t* __restrict__ ids, int T, int k,
+                                                                  int E, int32_t* __restrict__ offsets,
+                                                                  int32_t* __restrict__ active,
+                                                                  int32_t* __restrict__ sorted,
+                                                                  int32_t* __restrict__ pair_pos, TileOut to,
+                                                                  uint32_t* fork_sync, int withhold) {
+    sort_small(ids, T, k, E, offsets, active, sorted, pair_pos, to, fork_sync, withhold);
+}
+
+static_assert(kRouterPartsMaxT <= kSortChunk, "k_topk_group groups its tokens as one chunk");
+
+// The grouping's outputs for k_topk_group (as k_sort_small's arguments) and the workspace's sync words.
+struct GroupOut {
+    int32_t* offsets;
+    int32_t* active;
+    int32_t* sorted;
+    int32_t* pair_pos;
+    TileOut to;
+    uint32_t* sync;  // kTopkDone; the fork-scope words when fork
+    int fork;
+    int withhold;
+};
+
+// Top-k over the router's partials (k_topk_parts, one workgroup per token) followed by the grouping (k_sort_small)
+// in the same launch, for calls of at most kSortChunk tokens: each workgroup, once its token's picks are stored,
+// counts itself done in kTopkDone (a release at agent scope first); the last of the T then acquires and groups all
+// tokens' picks, and resets the count. One launch boundary fewer on the path before any expert work starts.
+template <int EJ, int NSEG>
+__global__ __launch_bounds__(1024) void k_topk_group(const float* __restrict__ parts, int nseg,
+                                                     const float* __restrict__ bias, int T, int E, int rows, int k,
+                                                     int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                     int32_t* __restrict__ corder, float* __restrict__ sg,
+                                                     GroupOut g) {
+    __shared__ int last;
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg);
+    __syncthreads();  // the picks are stored by wavefront 0, whose thread 0 counts the workgroup done
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const uint32_t prev = __hip_atomic_fetch_add(g.sync + kTopkDone, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        last = prev == static_cast<uint32_t>(T - 1) ? 1 : 0;
+        if (last) {
+            __hip_atomic_store(g.sync + kTopkDone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+    }
+    __syncthreads();
+    if (last)
+        sort_small(ids, T, k, E, g.offsets, g.active, g.sorted, g.pair_pos, g.to, g.fork ? g.sync : nullptr,
+                   g.withhold);
 }
 
 // Many chunks: one thread per expert turns its per-chunk counts (hist[c][e]) into the chunk's first sorted
@@ -1268,7 +1327,9 @@ static int launch_router_parts(const WlMoeLayer& L, const float* x, int64_t T, c
     return launch_status();
 }
 
-static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w, float* sg, hipStream_t s) {
+// With g, the grouping follows in the same launch (k_topk_group, 1024 threads: one per expert for the grouping).
+static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w, float* sg, const GroupOut* g,
+                             hipStream_t s) {
     const int rows = L.n_experts + ((L.shared_gate_up && L.shared_gate) ? 1 : 0);
     const int nseg = L.hidden / kRouterSeg;
     const int Ti = static_cast<int>(T);
@@ -1276,6 +1337,17 @@ static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w,
     const int E = L.n_experts, k = L.top_k, rn = L.norm_topk_prob ? 1 : 0;
     const unsigned threads = static_cast<unsigned>(rows + 63) / 64 * 64 < 1024u ? (rows + 63) / 64 * 64 : 1024u;
     // every instance has the same parameters; 32 segments: hidden 2048
+    if (g) {
+        auto pick = [&](auto seg32) {
+            constexpr int S = decltype(seg32)::value;
+            return E <= 64 ? k_topk_group<1, S> : E <= 128 ? k_topk_group<2, S> : E <= 256 ? k_topk_group<4, S>
+                   : E <= 512 ? k_topk_group<8, S> : k_topk_group<16, S>;
+        };
+        auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
+        kernel<<<grid, kSortSmallThreads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts,
+                                                  w.corder, sg, *g);
+        return launch_status();
+    }
     auto pick = [&](auto seg32) {
         constexpr int S = decltype(seg32)::value;
         return E <= 64 ? k_topk_parts<1, S> : E <= 128 ? k_topk_parts<2, S> : E <= 256 ? k_topk_parts<4, S>
@@ -1609,7 +1681,11 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         rc = launch_router_parts(L, x, tokens, w, mfma ? w.xb : nullptr, s);
         if (rc) return rc;
         mark(1);
-        rc = launch_topk_parts(L, tokens, w, sg, s);
+        // the grouping in the same launch (mark 3 follows mark 2 at once)
+        const GroupOut g{w.offsets, w.active, w.sorted, w.pair_pos,
+                         TileOut{mfma ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0, gemv_max},
+                         w.sync, in_scope ? 1 : 0, starve ? 1 : 0};
+        rc = launch_topk_parts(L, tokens, w, sg, &g, s);
         if (rc) return rc;
         mark(2);
     } else {
@@ -1622,8 +1698,10 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         if (rc) return rc;
         mark(2);
     }
-    rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, in_scope, starve, s);
-    if (rc) return rc;
+    if (!router_parts(tokens)) {
+        rc = launch_sort(L, w, w.ids, tokens, mfma, gemv_max, in_scope, starve, s);
+        if (rc) return rc;
+    }
     mark(3);
     const int max_gemv = plan == kPlanMfma ? 0 : static_cast<int>(P < L.n_experts ? P : L.n_experts);
     // the shared expert runs on the MFMA GEMMs in an MFMA plan (it sees every token), else on the GEMV kernels
