@@ -151,7 +151,8 @@ size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
 int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Zeroes the synchronization words at the start of a workspace (the fused decode kernel's per-workgroup epoch
- * counters and epoch-tagged exchange slots) with a fill kernel on `stream`. Call once after allocating a workspace, before its first
+ * counters and epoch-tagged exchange slots, the fork-scope words, the count of top-k workgroups done) with a fill
+ * kernel on `stream`. Call once after allocating a workspace, before its first
  * wl_moe_layer; calls keep these words consistent afterwards. Calls that share one workspace must be ordered (one
  * stream): concurrent ones race. */
 int wl_moe_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
