@@ -203,6 +203,22 @@ def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label, graph=True):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end)
     assert torch.isfinite(ys).all(), f"{label}: non-finite outputs"
+    checks = {}
+    if split:
+        # a fork-scope hand-off that gave up would skip the MFMA experts (stale outputs, little change in time):
+        # the workspace's status must be clean, and the last timed step must equal per-call runs bit for bit
+        st = layers[0].status(ws)
+        if st != 0:
+            raise SystemExit(f"{label}: a fork-scope wait gave up during the timed steps (status {st})")
+        last = xs[(steps - 1) % n_sets]
+        own = new_workspace(max(layer.workspace_bytes(T) for layer in layers), "cuda")
+        ref = torch.stack([layer(last[l], workspace=own) for l, layer in enumerate(layers)])
+        torch.cuda.synchronize()
+        if not torch.equal(ref, ys):
+            raise SystemExit(f"{label}: the timed step differs from per-call runs "
+                             f"(max diff {(ref - ys).abs().max().item():.3e})")
+        checks = {"status_after_timed_steps": st, "timed_step_equals_per_call_runs": True}
+        del ref, own
     U = unique_experts(torch, layers, xs, T)
     us_layer = ms * 1000.0 / (steps * L)
     bytes_layer = sum(layer_bytes(T, u) for u in U) / len(U)
@@ -211,7 +227,8 @@ def run_decode(torch, hip, layers, T, steps, warmup, n_sets, label, graph=True):
     del graphs
     return {"ms_per_step": ms / steps, "wall_s": wall, "us_per_layer": us_layer, "us_per_token_layer": us_layer / T,
             "bytes_per_layer": bytes_layer, "hbm_gbps": bytes_layer / us_layer / 1e3, "unique": U, "xs": xs,
-            "ws": ws, "launch": "hipGraph replay" if graph else ("eager, one fork scope per step" if split else "eager")}
+            "ws": ws, "launch": "hipGraph replay" if graph else ("eager, one fork scope per step" if split else "eager"),
+            **checks}
 
 
 def profile_stages(torch, hip, layers, xs, T, ws, reps=2):
@@ -560,9 +577,12 @@ def main():
     d1 = run_decode(torch, hip, layers, 1, args.steps, args.warmup, args.sets, "decode b=1",
                     graph=not args.no_graph)
     stages = profile_stages(torch, hip, layers, d1["xs"], 1, d1["ws"])
-    log("stage us (b=1): " + ", ".join(f"{k} {v:.2f}" for k, v in stages.items()))
     U1 = sum(d1["unique"]) / len(d1["unique"])
     plan = layers[0].plan(1)
+    if plan == "fused":  # one launch holds every stage: the events around it (eager) include the launch latency
+        log(f"b=1 fused kernel, events around single eager launches: {stages['router']:.2f} us per layer")
+    else:
+        log("stage us (b=1): " + ", ".join(f"{k} {v:.2f}" for k, v in stages.items()))
     if plan == "fused":
         # one kernel holds the whole layer, so the timed region is that kernel back to back: its events (on the
         # stream the graphs replay on) over the launch count give the launch duration, gaps between launches
@@ -611,7 +631,9 @@ def main():
                                 "us_per_layer": round(d64["us_per_layer"], 2),
                                 "hbm_gbps": round(d64["hbm_gbps"], 1),
                                 "mean_unique_experts": round(sum(d64["unique"]) / len(d64["unique"]), 1),
-                                "routing": "Zipf(1.1) router bias", "plan": zl[0].plan(64), "launch": d64["launch"]}
+                                "routing": "Zipf(1.1) router bias", "plan": zl[0].plan(64), "launch": d64["launch"],
+                                "status_after_timed_steps": d64.get("status_after_timed_steps"),
+                                "timed_step_equals_per_call_runs": d64.get("timed_step_equals_per_call_runs")}
         margins["config3_decode_b64"] = routing_margins(
             torch, torch.cat([layer_logits(torch, zl, xset) for xset in d64["xs"]]))
         del d64, zl

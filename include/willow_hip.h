@@ -145,7 +145,8 @@ size_t wl_moe_workspace_bytes(const WlMoeLayer* layer, int64_t tokens);
  * The fused kernel's hand-offs between workgroups need the whole grid resident at once; the library checks that
  * before it launches, and every wait is bounded, so a workgroup that still waits too long gives up, writes NaN for
  * its outputs and sets a status word. The waits of a fork scope (wl_moe_fork_begin) are bounded too; one that
- * gives up sets the word, and until it is cleared the scope's MFMA experts are skipped (their outputs are stale).
+ * gives up sets the word, and until it is cleared the scope's MFMA experts are skipped and every split-plan call
+ * in a scope writes NaN for its outputs (those experts' results would be stale).
  * This synchronizes `stream` (and, after a fork-scope wait gave up, the device), reads and clears the word, and
  * returns WL_OK, WL_ESYNC when it was set, or a hipError_t. Not for use under stream capture. */
 int wl_moe_workspace_status(void* workspace, size_t workspace_bytes, void* stream);

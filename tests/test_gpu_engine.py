@@ -133,3 +133,33 @@ def test_engine_model_loop(tokens):
         torch.cuda.synchronize()
         outs.append(xs)
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("tokens", [1, 40])  # 1: the fused kernel's exchange; 40: a fork-scope hand-off
+def test_engine_step_raises_on_give_up(small_layer, tokens):
+    """A bounded wait that gives up inside a decode step (forced from the host with WL_MOE_TEST_STARVE: a fused
+    workgroup or the grouping withholds its flag, and the waits give up after a short spin, so every kernel
+    exits) raises HipError when the step's scope ends, and the debug check after each layer raises too; once the
+    flag is cleared the next step is clean."""
+    from gguf import hip
+    lw = small_layer
+    store = HBMExpertStore.from_host([lw])
+    eng = TinyEngine(store, engine_weights(lw), lw["top_k"])
+    x = torch.from_numpy(synth.tokens(95 + tokens, tokens)).cuda()
+    view = eng.hip_layer(0)[0]
+    good = eng.moe(x, 0)
+    view.struct.flags |= hip.MOE_TEST_STARVE
+    print(f"[engine] forced give-up, T={tokens}", flush=True)
+    with pytest.raises(hip.HipError):
+        with eng.moe_step():
+            eng.moe(x, 0)
+    eng.moe_check_status = True  # now the check after the layer itself raises, inside the step
+    with pytest.raises(hip.HipError):
+        with eng.moe_step():
+            eng.moe(x, 0)
+    eng.moe_check_status = False
+    view.struct.flags &= ~hip.MOE_TEST_STARVE
+    with eng.moe_step():
+        again = eng.moe(x, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(again, good)

@@ -2,7 +2,8 @@
 library) against wl_moe_layer on the same inputs, through the C ABI: outputs and routing bit-identical, on calls
 in a row with shrinking inputs (the scratch keeps the previous call's contents), each plan covered (split MFMA +
 GEMV at 64 tokens, all-GEMV at 5, the fused kernel at 1); a call too large for the scratch is refused; split calls
-inside a fork scope equal the calls outside one."""
+made inside an open fork scope equal the calls outside one (they take no part in the scope: every call of this
+entry point runs its MFMA and GEMV experts on the caller's stream)."""
 import ctypes
 
 import numpy as np
@@ -50,11 +51,11 @@ def test_noalloc_refuses_oversize(hip, layer_c2):
 
 
 def test_noalloc_in_fork_scope(hip):
-    """Split-plan calls of the no-allocation entry point inside a fork scope, three layers in a row: the scratch
-    carries the scope's hand-off words as a shared workspace does, and the results equal the same calls outside a
-    scope bit for bit."""
+    """Split-plan calls of the no-allocation entry point made while a fork scope is open on the stream, three
+    layers in a row: they run unforked (the entry point never takes the second stream, so an open scope does not
+    change what it launches), and the results equal the same calls outside a scope bit for bit."""
     layers = [hip.MoELayer.from_host(synth.moe_layer(190 + i, experts=64, top_k=8)) for i in range(3)]
-    T = 40  # 64 experts, top-8: both expert classes, the second stream used
+    T = 40  # 64 experts, top-8: both expert classes (wl_moe_layer would use the second stream here)
     assert all(layer.plan(T) == "split" for layer in layers)
     xs = [torch.from_numpy(synth.tokens(1500 + i, T)).cuda() for i in range(3)]
     want = [layer(x) for layer, x in zip(layers, xs)]

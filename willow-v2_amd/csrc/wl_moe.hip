@@ -198,9 +198,14 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_router_parts(const float* __r
                                                                 const float* __restrict__ w,
                                                                 const float* __restrict__ shared_gate, int T,
                                                                 int H, int E, float* __restrict__ parts,
-                                                                uint16_t* __restrict__ xb) {
+                                                                uint16_t* __restrict__ xb,
+                                                                uint32_t* __restrict__ topk_done) {
     __shared__ __attribute__((aligned(16))) float stage[kRsWaves][2][kRsTile];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // the count k_topk_group (next on this stream) starts from: zeroed here by every call, so a workspace whose
+    // words were never initialised still groups (its last-workgroup test only needs the count to start at 0)
+    if (topk_done && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+        __hip_atomic_store(topk_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
     const int rows = E + (shared_gate ? 1 : 0);
     const int seg = static_cast<int>(blockIdx.z) * kRsWaves + wv;
@@ -495,6 +500,19 @@ __global__ __launch_bounds__(64) void k_fork_wait(uint32_t* sync, uint32_t spin_
     else
         __hip_atomic_fetch_or(sync + kStatusWord, kStatusFork, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(sync + kForkSkip, ok ? 0u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The caller's stream's wait for the second stream's MFMA experts (one thread; at most spin_limit polls): the
+// combine is launched after this kernel, so no workgroup of a wide grid holds a CU while the MFMA kernels may still
+// need it. Relaxed polls; the combine acquires at its start. A wait that gives up sets kStatusFork.
+__global__ __launch_bounds__(64) void k_fork_gate(uint32_t* sync, uint32_t spin_limit) {
+    if (threadIdx.x != 0) return;
+    bool ok = false;
+    for (uint32_t spins = 0; spins < spin_limit && !ok; spins++) {
+        ok = __hip_atomic_load(sync + kForkDone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+        if (!ok) __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) __hip_atomic_fetch_or(sync + kStatusWord, kStatusFork, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
@@ -1091,22 +1109,17 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
                                                  const float* __restrict__ wts, const float* __restrict__ o,
                                                  const SH* __restrict__ o_sh, const float* __restrict__ sg,
                                                  const float* __restrict__ resid, float* __restrict__ y,
-                                                 uint32_t* fork_sync, uint32_t spin_limit) {
-    if (fork_sync) {  // fork scope: the MFMA experts' outputs come from the second stream (at most spin_limit
-                      // relaxed polls, then one acquire for the workgroup's reads)
-        if (threadIdx.x == 0) {
-            bool ok = false;
-            for (uint32_t spins = 0; spins < spin_limit && !ok; spins++) {
-                ok = __hip_atomic_load(fork_sync + kForkDone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
-                if (!ok) __builtin_amdgcn_s_sleep(1);
-            }
-            if (!ok)
-                __hip_atomic_fetch_or(fork_sync + kStatusWord, kStatusFork, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_SYSTEM);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        }
+                                                 const uint32_t* status) {
+    // fork scope (status: the workspace's status word). k_fork_gate, just before on this stream, has seen the MFMA
+    // experts done; one acquire drops any line of their outputs this XCD's caches still hold from an earlier call.
+    // Once a hand-off has given up, those outputs are stale, so every output is NaN until wl_moe_workspace_status
+    // has reported it.
+    if (status) {
+        if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         __syncthreads();
     }
+    const bool stale =
+        status && (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kStatusFork) != 0;
     const int spans = (H + kCombineSpan - 1) / kCombineSpan;
     const int t = static_cast<int>(blockIdx.x) / spans;
     const int r = (static_cast<int>(blockIdx.x) - t * spans) * kCombineSpan + 8 * static_cast<int>(threadIdx.x);
@@ -1185,6 +1198,11 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
                          __fadd_rn(xv.a.w, a0.w));
         a1 = make_float4(__fadd_rn(xv.b.x, a1.x), __fadd_rn(xv.b.y, a1.y), __fadd_rn(xv.b.z, a1.z),
                          __fadd_rn(xv.b.w, a1.w));
+    }
+    if (stale) {
+        const float q = __builtin_nanf("");
+        a0 = make_float4(q, q, q, q);
+        a1 = a0;
     }
     float* out = y + static_cast<int64_t>(t) * H + r;
     *reinterpret_cast<float4*>(out) = a0;
@@ -1323,7 +1341,7 @@ static int launch_router_parts(const WlMoeLayer& L, const float* x, int64_t T, c
     k_router_parts<<<dim3(static_cast<unsigned>((T + 15) / 16), static_cast<unsigned>((rows + 15) / 16),
                           static_cast<unsigned>((nseg + kRsWaves - 1) / kRsWaves)),
                      64 * kRsWaves, 0, s>>>(x, L.router, shared_gate, static_cast<int>(T), L.hidden, L.n_experts,
-                                            w.parts, xb);
+                                            w.parts, xb, w.sync + kTopkDone);
     return launch_status();
 }
 
@@ -1747,18 +1765,22 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         if (e != hipSuccess) return static_cast<int>(e);
     }
     if (fork_guard.owns_lock()) fork_guard.unlock();
-    uint32_t* combine_wait = in_scope ? w.sync : nullptr;
+    if (in_scope) {  // the combine follows the MFMA experts' kForkDone (a one-thread gate on this stream)
+        k_fork_gate<<<1, 64, 0, s>>>(w.sync, kForkSpin);
+        rc = launch_status();
+        if (rc) return rc;
+    }
+    const uint32_t* combine_status = in_scope ? w.sync + kStatusWord : nullptr;
     mark(5);
     const unsigned cgrid = static_cast<unsigned>(tokens * ((L.hidden + kCombineSpan - 1) / kCombineSpan));
     if (mfma)
         k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
                                                   w.wts, w.o,
                                                   shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg,
-                                                  resid, y, combine_wait, kForkSpin);
+                                                  resid, y, combine_status);
     else
         k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y, combine_wait,
-                                               kForkSpin);
+                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y, combine_status);
     rc = launch_status();
     mark(6);
     return rc;

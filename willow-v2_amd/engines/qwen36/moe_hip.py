@@ -24,10 +24,12 @@ they are dense tensors (the reference's loader dequantizes them to bf16, engines
 routed part runs fused and the shared expert is added with the reference's own formula (engines/base.py:104-107).
 Arithmetic is fp32 inside the kernel; the result is cast back to x's dtype.
 """
+import contextlib
+
 import torch
 import torch.nn.functional as F
 
-from gguf.hip import GGMLWeight, fork_scope
+from gguf.hip import ESYNC, GGMLWeight, HipError, fork_scope, library
 
 
 def dense_shared_expert(x, gate_w, up_w, down_w, shared_gate_w):
@@ -74,11 +76,27 @@ class HipMoE:
         cache[layer] = (view, dense)
         return cache[layer]
 
+    @contextlib.contextmanager
     def moe_step(self):
-        """A context for one decode step's layers: the library's fork scope on the experts' device."""
-        return fork_scope(self.experts.device)
+        """A context for one decode step's layers: the library's fork scope on the experts' device. On leaving it,
+        every layer's workspace status is read (one stream synchronization), and a bounded wait that gave up inside
+        the step (the MFMA experts of a hand-off skipped, or a fused-kernel exchange: outputs NaN) raises HipError,
+        so such outputs never pass into the residual stream unnoticed."""
+        with fork_scope(self.experts.device):
+            yield
+        self.check_moe_status()
+
+    def check_moe_status(self):
+        """Raises HipError (code ESYNC) when a bounded wait of any built layer gave up since the last check."""
+        for layer, (view, _) in sorted(self.__dict__.get("_hip_moe_layers", {}).items()):
+            if view.status() == ESYNC:
+                raise HipError(ESYNC, f"layer {layer}: " + library().wl_error_string(ESYNC).decode())
 
     def moe(self, x: torch.Tensor, layer: int, residual: torch.Tensor = None) -> torch.Tensor:
+        if getattr(self, "min_expert_weight", 0.0):
+            # engines/base.py:413-430,463-464 (skip_small_experts): not run on this backend; refusing keeps a run
+            # with --min-expert-weight from silently computing every routed expert
+            raise NotImplementedError("min_expert_weight (skip_small_experts) is not supported by the HIP MoE layer")
         view, dense = self.hip_layer(layer)
         nxt = layer + 1
         if getattr(view, "_next", None) is None and nxt < len(getattr(self.experts, "layers", ())):
@@ -90,4 +108,6 @@ class HipMoE:
         if dense is not None:
             gate_w, up_w, down_w, gate_g = dense
             out = out + dense_shared_expert(flat.to(gate_w.dtype), gate_w, up_w, down_w, gate_g).float()
+        if getattr(self, "moe_check_status", False):  # debug: read the status after every layer (a sync each)
+            self.check_moe_status()
         return out.to(device=x.device, dtype=x.dtype).view_as(x)
