@@ -267,16 +267,16 @@ def run_chained(torch, hip, layers, steps, warmup, n_sets):
     """Decode b=1 with each layer's input the previous layer's output, as the model chains them:
     x_{l+1} = x_l + MoE_l(rms_norm_l(x_l)) (engines/qwen36/model.py:22; the attention half is not part of this
     path). One launch per layer (the layer's pre-norm and residual flags), the stack captured as one graph per
-    starting vector and replayed; the graph's output is checked bit for bit against an eager pass. Also measures
-    how often the reference's next-layer guess, layer l+1's router on rms_norm_{l+1}(x_l) before layer l's experts
-    are added (engines/base.py:392-406, engines/qwen36/model.py:30-31), names layer l+1's actual experts."""
+    starting vector and replayed; the graph's output is checked bit for bit against an eager pass. Timed twice in
+    the same session: without and with the next-layer guess (WL_MOE_GUESS_NEXT: layer l also computes layer l+1's
+    router on rms_norm_{l+1}(x_l), the reference's guess_next_layer, engines/base.py:392-406 with
+    engines/qwen36/model.py:30-31, and pulls the guessed experts' gate_up rows into the caches); both give the same
+    bits. Also measures how often that guess names layer l+1's actual experts."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4242)
     L = len(layers)
     norm_w = [torch.randn(HIDDEN, device="cuda", generator=gen) * 0.1 for _ in range(L)]
     chain = [layer.with_norm(norm_w[l]) for l, layer in enumerate(layers)]
-    for l in range(L):
-        chain[l].set_next(chain[(l + 1) % L])
     x0 = [torch.randn(1, HIDDEN, device="cuda", generator=gen) for _ in range(n_sets)]
     xs = torch.empty(L, 1, HIDDEN, device="cuda")  # layer l writes x_{l+1} into xs[l]
     ws = new_workspace(max(layer.workspace_bytes(1) for layer in chain), "cuda")
@@ -286,50 +286,72 @@ def run_chained(torch, hip, layers, steps, warmup, n_sets):
             layer(x if l == 0 else xs[l - 1], out=xs[l], workspace=ws, ids=None if ids is None else ids[l])
 
     ids = torch.empty(n_sets, L, 1, TOP_K, dtype=torch.int32, device="cuda")
+
+    def measure(guess):
+        # the last layer's next is the first (the next step's layer 0, whose input is a new token: no guess there)
+        for l in range(L):
+            chain[l].set_next(chain[(l + 1) % L], guess=guess and l + 1 < L)
+        eager_out = []
+        for s in range(n_sets):
+            stack(x0[s], ids[s])
+            eager_out.append(xs[L - 1].clone())
+        torch.cuda.synchronize()
+        graphs = []
+        capture = torch.cuda.Stream()
+        for s in range(n_sets):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=capture):
+                stack(x0[s])
+            graphs.append(g)
+        for s in range(n_sets):
+            graphs[s].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(xs[L - 1], eager_out[s]), "chained decode: graph replay differs from the eager pass"
+        for i in range(warmup):
+            graphs[i % n_sets].replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            graphs[i % n_sets].replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        assert torch.isfinite(xs).all(), "chained decode: non-finite outputs"
+        status = chain[0].status(ws)
+        assert status == 0, f"chained decode: workspace status {status} after the timed steps"
+        del graphs
+        return ms, eager_out
+
+    ms_plain, out_plain = measure(False)
+    ms_guess, out_guess = measure(True)
+    for s in range(n_sets):
+        assert torch.equal(out_plain[s], out_guess[s]), "chained decode: the next-layer guess changed the outputs"
     hits = []
-    eager_out = []
-    for s in range(n_sets):  # eager passes: routing of every layer, and each step's last output
+    for s in range(n_sets):  # the routing of every layer (ids of the last eager pass of each set), then the guess
         stack(x0[s], ids[s])
         for l in range(L - 1):
             x_l = x0[s] if l == 0 else xs[l - 1]
             _, guess, _ = layers[l + 1].route(rms_norm_torch(torch, x_l, norm_w[l + 1]))
             hits.append(torch.isin(guess[0], ids[s, l + 1, 0]).sum())
-        eager_out.append(xs[L - 1].clone())
     torch.cuda.synchronize()
-    hit_rate = float(torch.stack(hits).sum()) / (len(hits) * TOP_K)
-    graphs = []
-    capture = torch.cuda.Stream()
-    for s in range(n_sets):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=capture):
-            stack(x0[s])
-        graphs.append(g)
-    for s in range(n_sets):
-        graphs[s].replay()
-        torch.cuda.synchronize()
-        assert torch.equal(xs[L - 1], eager_out[s]), "chained decode: graph replay differs from the eager pass"
-    for i in range(warmup):
-        graphs[i % n_sets].replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        graphs[i % n_sets].replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    assert torch.isfinite(xs).all(), "chained decode: non-finite outputs"
+    hits = torch.stack(hits)
+    hit_rate = float(hits.sum()) / (len(hits) * TOP_K)
+    all_hit = float((hits == TOP_K).float().mean())  # layers whose experts the guess names all of
     for layer in chain:
         layer.set_next(None)
-    us_layer = ms * 1000.0 / (steps * L)
+    us_plain = ms_plain * 1000.0 / (steps * L)
+    us_guess = ms_guess * 1000.0 / (steps * L)
     bytes_layer = layer_bytes(1, TOP_K)
-    log(f"decode b=1 chained: {ms / steps:.3f} ms/step, {us_layer:.2f} us/layer, "
-        f"{bytes_layer / us_layer / 1e3:.0f} GB/s, next-layer guess hit rate {hit_rate:.3f}")
-    del graphs
-    return {"us_per_token_layer": round(us_layer, 3), "ms_per_step": round(ms / steps, 4),
-            "hbm_gbps": round(bytes_layer / us_layer / 1e3, 1), "steps": steps, "starting_vectors": n_sets,
+    log(f"decode b=1 chained: {us_plain:.2f} us/layer ({bytes_layer / us_plain / 1e3:.0f} GB/s); with the next-layer "
+        f"guess {us_guess:.2f} us/layer; guess hit rate {hit_rate:.3f}")
+    return {"us_per_token_layer": round(us_plain, 3), "ms_per_step": round(ms_plain / steps, 4),
+            "hbm_gbps": round(bytes_layer / us_plain / 1e3, 1), "steps": steps, "starting_vectors": n_sets,
             "graph_matches_eager": True, "next_layer_guess_hit_rate": round(hit_rate, 4),
+            "next_layer_guess_all_hit": round(all_hit, 4),
             "guess": "top-8 of layer l+1's router on rms_norm_{l+1}(x_l), scored against layer l+1's experts",
+            "with_next_layer_guess": {"us_per_token_layer": round(us_guess, 3), "same_outputs": True,
+                                      "flag": "WL_MOE_GUESS_NEXT (guessed experts' gate_up rows pulled into L2)"},
             "norm": "zero-centered RMSNorm, weights N(0, 0.1), eps 1e-6"}
 
 

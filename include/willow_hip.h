@@ -131,6 +131,16 @@ typedef struct WlMoeLayer {
 #define WL_MOE_PRE_NORM 16       /* flags: run on rms_norm(x) (norm_weight, norm_eps; see WlMoeLayer) */
 #define WL_MOE_RESIDUAL 32       /* flags: y = x + MoE(input), the residual add of engines/qwen36/model.py:22; y and
                                     x must not overlap */
+#define WL_MOE_GUESS_NEXT 64     /* flags, batch-1 decode with WL_MOE_PRE_NORM: the next call on this workspace is
+                                    `next`, on an input derived from this call's x (the model's decoder loop). The
+                                    fused kernel then also computes the next layer's router on rms_norm_next(x) (its
+                                    norm weight and eps) and leaves it in the workspace; the next call (with this
+                                    flag too) takes its top-k as a guess of its experts and pulls their gate_up rows
+                                    into the GPU's caches before its routing is known: the early read of
+                                    guess_next_layer (engines/base.py:392-406,472-474). Results are unchanged; on
+                                    the MI355X it measured slower (1.5 us per layer), so it is off unless asked for.
+                                    Ignored unless `next` has the same shapes and WL_MOE_PRE_NORM too, and outside
+                                    256 experts of width 512. */
 #define WL_MOE_TEST_STARVE 8     /* flags, testing only: in the fused kernel one workgroup withholds its results and
                                     the others' bounded waits give up early, so the call ends with NaN outputs and
                                     the workspace's status word set (the failure wl_moe_workspace_status reports) */

@@ -320,6 +320,65 @@ def test_fused_give_up_is_reported(hip, layer_c2):
     assert moe_ref.rel_err(y, moe_ref.layer(x, layer_c2)) < TOL
 
 
+# The fused kernel's guess logits in a workspace: two sets of 256 64-bit words (call tag << 32 | float bits) at this
+# 32-bit word offset, after the per-workgroup epoch lines (32 words x 512), the tagged logits (2 x 272), h_shared
+# (2 x 1024), h (2 x 8 x 1024), the status line and the four fork / top-k lines (32 words each).
+GUESS_WORD = 32 * 512 + 2 * 272 + 2 * 1024 + 2 * 8 * 1024 + 5 * 32
+
+
+def latest_guess(ws):
+    """The guess logits of the most recent call that left one: the set whose 256 tags are that call's."""
+    words = ws[4 * GUESS_WORD:4 * (GUESS_WORD + 2 * 2 * 256)].cpu().numpy().view(np.uint32).reshape(2, 256, 2)
+    tags = words[:, :, 1]
+    s = int(np.argmax(tags[:, 0]))
+    assert (tags[s] == tags[s, 0]).all() and tags[s, 0] > 0
+    return words[s, :, 0].view(np.float32).copy()
+
+
+def test_next_layer_guess(hip, c2, layer_c2):
+    """WL_MOE_GUESS_NEXT, the early read of guess_next_layer (engines/base.py:392-406,472-474): three chained
+    decoder steps x_{l+1} = x_l + MoE_l(rms_norm_l(x_l)) of the full-shape layer (a different norm weight per
+    layer, so each routes differently). The guess only pulls rows into the caches, so every output and routing
+    equals the chain without it bit for bit. The guess itself: the next layer's logits the kernel leaves in its
+    workspace equal the oracle's fixed-order router on rms_norm_{l+1}(x_l) (the reference's router_guess_input,
+    engines/qwen36/model.py:30-31) bit for bit."""
+    rng = np.random.default_rng(17)
+    norm_w = [(rng.standard_normal(2048) * 0.1).astype(np.float32) for _ in range(3)]
+    x0 = synth.tokens(77, 1) * np.float32(2.0)
+    runs = {}
+    for guess in (False, True):
+        chain = [c2.with_norm(torch.from_numpy(w).cuda()) for w in norm_w]
+        for l in range(2):
+            chain[l].set_next(chain[l + 1], guess=guess)
+        ws = chain[0].workspace(1)
+        x = torch.from_numpy(x0).cuda()
+        xs, ys, idss, guess_logits = [], [], [], []
+        for l, layer in enumerate(chain):
+            print(f"[moe] next-layer guess={guess}: layer {l}", flush=True)
+            ids = torch.empty(1, 8, dtype=torch.int32, device="cuda")
+            y = layer(x, ids=ids, workspace=ws)
+            torch.cuda.synchronize()
+            if guess and l < 2:
+                guess_logits.append(latest_guess(ws))
+            xs.append(x.cpu().numpy())
+            ys.append(y.cpu().numpy())
+            idss.append(ids.cpu().numpy())
+            x = y
+        assert layer.status(ws) == 0
+        runs[guess] = (xs, ys, idss, guess_logits)
+    for l in range(3):
+        np.testing.assert_array_equal(runs[True][2][l], runs[False][2][l])
+        np.testing.assert_array_equal(runs[True][1][l].view(np.uint32), runs[False][1][l].view(np.uint32))
+    xs, ys, _, guess_logits = runs[True]
+    for l in range(2):
+        want = cref.router_logits(moe_ref.rms_norm(xs[l], norm_w[l + 1], 1e-6), layer_c2["router"])[0]
+        np.testing.assert_array_equal(guess_logits[l].view(np.uint32), want.view(np.uint32))
+    # the chain itself against the oracle, layer by layer
+    for l in range(3):
+        y_ref = xs[l] + moe_ref.layer(moe_ref.rms_norm(xs[l], norm_w[l], 1e-6), layer_c2)
+        assert moe_ref.rel_err(ys[l], y_ref) < TOL
+
+
 @pytest.fixture(scope="module")
 def c2_norm_weight():
     return (np.random.default_rng(5).standard_normal(2048) * 0.1).astype(np.float32)

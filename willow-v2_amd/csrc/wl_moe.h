@@ -42,7 +42,11 @@ constexpr int kForkSkip = kForkDone + kFlagStride;
 // and the count of top-k workgroups done in a call of 2 .. kRouterPartsMaxT tokens (the last one runs the grouping
 // and resets it to 0)
 constexpr int kTopkDone = kForkSkip + kFlagStride;
-constexpr int kSyncWords = kTopkDone + kFlagStride;
+// the fused kernel's next-layer guess (WL_MOE_GUESS_NEXT): the next layer's router logits on this layer's input,
+// tagged 64-bit values [2][E]: a call with tag t writes set t & 1 and reads the previous call's guess from the
+// other set, so no call overwrites a set that a call still running reads
+constexpr int kTagGuess = kTopkDone + kFlagStride;
+constexpr int kSyncWords = kTagGuess + 2 * 2 * kFusedMaxE;
 
 struct ExpertArgs {
     const uint8_t* gate_up;

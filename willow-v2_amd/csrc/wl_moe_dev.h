@@ -264,6 +264,39 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lt, int E, i
     out_w = pick_weight(my_v, m, s, k, renorm, lane);
 }
 
+// The ids of k of the largest values in v (lane l holds values l + 64 j, j < EJ, as order keys; 0 = no value),
+// written to out[r] for r < k in descending order of value (one wavefront, 1 <= k <= the number of values).
+// k rounds of a wave maximum (DPP within rows, then the row maxima); in each, the lowest lane holding the maximum
+// gives up one value holding it. Equal values are taken in an unspecified order: for a guess, not a routing.
+template <int EJ>
+__device__ __forceinline__ void select_top_keys(uint32_t (&key)[EJ], int k, int lane, int* out) {
+    for (int r = 0; r < k; r++) {
+        uint32_t m = key[0];
+#pragma unroll
+        for (int j = 1; j < EJ; j++) m = max(m, key[j]);
+        int u = static_cast<int>(m);
+        u = umax_dpp<0xB1>(u);   // quad_perm [1,0,3,2]
+        u = umax_dpp<0x4E>(u);   // quad_perm [2,3,0,1]
+        u = umax_dpp<0x141>(u);  // row_half_mirror
+        u = umax_dpp<0x140>(u);  // row_mirror: every lane holds its row's maximum
+        const uint32_t M = max(max(static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 0)),
+                                   static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 16))),
+                               max(static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 32)),
+                                   static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 48))));
+        const int owner = __builtin_ctzll(__ballot(m == M));
+        if (lane == owner) {
+            int jj = 0;
+#pragma unroll
+            for (int j = EJ - 1; j >= 0; j--)
+                if (key[j] == M) jj = j;
+            out[r] = lane + 64 * jj;
+#pragma unroll
+            for (int j = 0; j < EJ; j++)
+                if (j == jj) key[j] = 0;
+        }
+    }
+}
+
 // One intermediate row j of a fused [gate | up] matrix (gate row j, up row inter + j) times one token x, one
 // wavefront; every lane returns the two sums.
 template <int TYPE>

@@ -79,6 +79,15 @@ struct FusedArgs {
     const float* norm_w;  // NORM: the RMSNorm weight (zero-centered) or NULL
     float norm_eps;
     int residual;         // y = x + MoE
+    // the next-layer guess (NORM only). Producer (guess_router non-NULL): the next layer's router (and bias) on this
+    // layer's x normalized with the next layer's RMSNorm (weight or NULL, eps), one row per workgroup while it waits
+    // for h, left in the workspace. Consumer (consume_guess): the previous call's guess on this workspace, read
+    // as this call starts; its top-k names the experts whose gate_up rows this call pulls into the caches
+    const float* guess_router;
+    const float* guess_bias;
+    const float* guess_norm_w;
+    float guess_eps;
+    int consume_guess;
 };
 
 // The 128-byte lines of what wavefront slot t reads in phase A (router row t, or the shared expert's gate row j and
@@ -165,7 +174,7 @@ __device__ __forceinline__ bool gather_tagged_wave(const uint32_t* sync, uint32_
     }
 }
 
-template <int GU, int DN, int EJ, int NBD, bool NORM>
+template <int GU, int DN, int EJ, int NBD, bool NORM, bool GUESS>
 __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     constexpr int WIDTH = 8 * NBD;  // lanes per down row (8 per block)
     constexpr int R = 64 / WIDTH;   // down rows per wavefront pass
@@ -179,6 +188,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ __attribute__((aligned(16))) float lds_xn[NORM ? kFusedMaxHidden : 4];  // NORM: the normalized x
+    // GUESS (the next-layer guess): x normalized with the next layer's RMSNorm; the previous call's guess (ids)
+    __shared__ __attribute__((aligned(16))) float lds_xg[GUESS ? kFusedMaxHidden : 4];
+    __shared__ int lds_gsel[GUESS ? kFusedMaxK : 1];
+    __shared__ int lds_gvalid;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int b = blockIdx.x, G = a.G;
     const int H = a.H, I = a.I, E = a.E, k = a.k;
@@ -217,22 +230,32 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                 wpre[i] = reinterpret_cast<const float4*>(wr0 + lane * kRouterSeg)[i];
         }
     }
+    const bool guess = GUESS && a.guess_router != nullptr;
     if constexpr (NORM) {
-        __shared__ float lds_inv;
+        __shared__ float lds_inv, lds_inv_g;
         const bool mine = static_cast<int>(threadIdx.x) < H / 4;
-        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), nw = xv;
+        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), nw = xv, gw = xv;
         if (mine) {
             xv = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
             if (a.norm_w) nw = reinterpret_cast<const float4*>(a.norm_w)[threadIdx.x];
+            if (guess && a.guess_norm_w) gw = reinterpret_cast<const float4*>(a.guess_norm_w)[threadIdx.x];
             reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = xv;
         }
         __syncthreads();
         if (wv == 0) {
             const float ss = router_row(lds_xn, lds_xn, true, H, lane);
-            if (lane == 0) lds_inv = norm_inv(ss, H, a.norm_eps);
+            if (lane == 0) {
+                lds_inv = norm_inv(ss, H, a.norm_eps);
+                lds_inv_g = norm_inv(ss, H, a.guess_eps);  // the same x: only the weight and eps differ
+            }
         }
         __syncthreads();
-        if (mine) reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = norm_apply(xv, a.norm_w != nullptr, nw, lds_inv);
+        if (mine) {
+            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = norm_apply(xv, a.norm_w != nullptr, nw, lds_inv);
+            if (guess)
+                reinterpret_cast<float4*>(lds_xg)[threadIdx.x] = norm_apply(xv, a.guess_norm_w != nullptr, gw,
+                                                                            lds_inv_g);
+        }
         __syncthreads();
     }
     auto xload = [&](int i) -> float4 {
@@ -271,6 +294,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     const bool owner = b < H / kOwnRows;
     const bool sh_wave = wv < kOwnRows / R;
     RawLane<DN> shraw;
+    uint32_t touched = 0;  // prefetch loads: consumed (never used) at the very end, so they are kept
 
     // phase A: router rows, shared gate_up rows
     const int n_router = n_logits;  // one router row per wavefront task (lanes 0..31), more tasks in parallel
@@ -300,11 +324,40 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             if (lane == 0 && publish) put_tagged(a.sync, kTagHsh + 2 * j, tag, silu(g) * u);
         }
     }
-
     // the shared down rows: requested only now, after phase A, whose router rows would otherwise queue behind them
     if (shared && sh_wave && owner)
         shraw.fetch(a.sh_down + static_cast<int64_t>(kOwnRows * b + R * wv + drow) * dn_rs +
                         kb * BlockInfo<DN>::bytes, c);
+
+    // the previous call's next-layer guess (a decoder loop's previous layer, WL_MOE_GUESS_NEXT), read in the last
+    // wavefront, which has no phase A task: when every guess logit the previous call left in the workspace carries
+    // that call's tag, their top-k (the guessed experts) goes to LDS for the prefetch below.
+    const int lpr = static_cast<int>((gu_rs + 127) / 128);  // 128-byte lines per gate_up row
+    const int nrj = (I - b + G - 1) / G;                     // this workgroup's gate_up rows j = b + G m < I
+    if constexpr (GUESS) {
+        if (a.consume_guess && wv == kFusedWaves - 1) {
+            const uint32_t prev = tag - 1u;
+            const int set = static_cast<int>(prev & 1u);
+            bool fresh = true;
+            uint32_t key[EJ];
+#pragma unroll
+            for (int j = 0; j < EJ; j++) {
+                const int idx = lane + 64 * j;
+                key[j] = 0u;
+                if (idx < E) {
+                    const uint64_t w = __hip_atomic_load(
+                        reinterpret_cast<const uint64_t*>(a.sync + kTagGuess + 2 * (set * kFusedMaxE + idx)),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    fresh = fresh && static_cast<uint32_t>(w >> 32) == prev;
+                    const float v = __builtin_bit_cast(float, static_cast<uint32_t>(w));
+                    key[j] = order_key(v == v ? v : -INFINITY);
+                }
+            }
+            const bool valid = __all(fresh);
+            if (valid) select_top_keys<EJ>(key, k, lane, lds_gsel);
+            if (lane == 0) lds_gvalid = valid ? 1 : 0;
+        }
+    }
 
     // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
     // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading.
@@ -314,6 +367,24 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
              [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
              [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
          ok;
+    // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
+    // slot u mod (8 G), so on workgroup u mod G: rows j = b, b + G, ... and their up rows), one 4-byte load per
+    // 128-byte line, spread over wavefronts 1 .. 7 while wavefront 0 runs the top-k: HBM carries nothing else then,
+    // and the lines reach this XCD's L2 before the loads below ask for them.
+    if constexpr (GUESS) {
+        if (a.consume_guess && wv > 0 && lds_gvalid) {
+            const int per_e = 2 * nrj * lpr, lines = k * per_e;
+            for (int L = lane + 64 * (wv - 1); L < lines; L += 64 * (kFusedWaves - 1)) {
+                const int s = L / per_e, rl = L - s * per_e, r = rl / lpr, ln = rl - r * lpr;
+                const int j = b + G * (r < nrj ? r : r - nrj);
+                const int row = r < nrj ? j : I + j;
+                const int64_t off = static_cast<int64_t>(row) * gu_rs +
+                                    (ln + 1 < lpr ? 128 * ln : static_cast<int>(gu_rs) - 4);
+                touched ^= *reinterpret_cast<const uint32_t*>(
+                    a.gate_up + static_cast<int64_t>(lds_gsel[s]) * a.gate_up_stride + off);
+            }
+        }
+    }
     // top-k, in wavefront 0. Lane l holds logits l + 64 j. The 8 groups of 32 logits (j, half of the wavefront)
     // reduce their order keys to the maximum (DPP within rows of 16, then a row broadcast); with T0 the smallest
     // maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at least k the
@@ -488,10 +559,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // next-layer overlap: the lines this wavefront's phase A task reads in the next layer (and, in the last
     // wavefront, the next layer's shared down rows of this owner), requested now: this wavefront's first h poll
     // below would not succeed before they arrive anyway. Consumed (never used) at the very end.
-    uint32_t touched = 0;
     if (a.next_router) {
         const int t = slot;
-        if (t < n_router) {
+        if (guess && t < E) {
+            // guess_rows computes this row of the next layer's router on this workgroup
+        } else if (t < n_router) {
             const float* wr = t < E ? a.next_router + static_cast<int64_t>(t) * H : a.next_sh_gate;
             touched = touch_lines(reinterpret_cast<const uint8_t*>(wr), 4 * H, lane);
         } else if (t < n_a) {
@@ -506,6 +578,23 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if (wv == kFusedWaves - 2 && a.next_norm_w)  // every workgroup reads all of it first thing
             touched ^= touch_lines(reinterpret_cast<const uint8_t*>(a.next_norm_w), 4 * H, lane);
     }
+    // the next-layer guess (producer): the next layer's router rows e = b, b + G, ... on x normalized with that
+    // layer's RMSNorm (router_row's order, then the bias), computed while this wavefront waits for h (after its
+    // down rows are requested) and left in the workspace's guess set tag & 1 for the next call. The wavefront is
+    // one of the first picked experts', whose h comes from the first gate_up tasks and so is gathered earlier. Row e
+    // is computed on the workgroup whose wavefront slot e reads it in the next layer's phase A (workgroup e mod G,
+    // the same XCD), so this also stands for that row's prefetch.
+    const int guess_wave = k > 1 ? 1 : 0;
+    auto guess_rows = [&]() {
+        for (int e = b; e < E; e += G) {
+            const float total = router_row_x([&](int i) { return reinterpret_cast<const float4*>(lds_xg)[i]; },
+                                             a.guess_router + static_cast<int64_t>(e) * H, lane < 32, H, lane);
+            if (lane == 0 && publish)
+                put_tagged(a.sync, kTagGuess + 2 * (static_cast<int>(tag & 1u) * kFusedMaxE + e), tag,
+                           a.guess_bias ? __fadd_rn(total, a.guess_bias[e]) : total);
+        }
+    };
+    if (guess && wv == guess_wave && !(owner && wv < k)) guess_rows();
     if (owner && wv < k) {
         auto own_row = [&](int pass) { return kOwnRows * b + R * pass + drow; };
         RawLane<DN> draw[NBD];
@@ -513,6 +602,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
 #pragma unroll
         for (int p = 0; p < NBD; p++)
             draw[p].fetch(w + static_cast<int64_t>(own_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
+        if (guess && wv == guess_wave) guess_rows();
         float* hs = lds_h[wv];
         ok = gather_tagged_wave<4 * NBD>(
                  a.sync, tag, a.spin_limit, [&](int i) { return kTagH + 2 * (wv * I + i); },
@@ -557,22 +647,33 @@ __global__ void k_zero_words(uint32_t* p, int n) {
 // ---------------------------------------------------------------------------------------------------------------
 
 // The fused kernel instance a layer runs: gate_up Q4_K; down Q4_K or Q6_K; EJ logits per lane of the top-k; NBD
-// down blocks per row (inter / 256).
+// down blocks per row (inter / 256). The next-layer guess (WL_MOE_GUESS_NEXT with the pre-norm) has instances of
+// its own, at Qwen3.6's shapes only (elsewhere the flag is ignored), so the code of the other instances is the same
+// as without it.
+static bool guess_instance(const WlMoeLayer& L) {
+    return (L.flags & WL_MOE_GUESS_NEXT) && (L.flags & WL_MOE_PRE_NORM) && L.n_experts > 128 &&
+           L.n_experts <= 256 && L.inter == 2 * kQK;
+}
+
 static const void* fused_instance(const WlMoeLayer& L) {
     const int ej = L.n_experts <= 64 ? 1 : L.n_experts <= 128 ? 2 : 4;
     const int nbd = L.inter / kQK;
     const bool norm = (L.flags & WL_MOE_PRE_NORM) != 0;
+    if (guess_instance(L))
+        return L.down_type == WL_TYPE_Q4_K
+                   ? reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, WL_TYPE_Q4_K, 4, 2, true, true>)
+                   : reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, WL_TYPE_Q6_K, 4, 2, true, true>);
 #define WL_FUSED_PICK(DN, NORM)                                                                                    \
     switch (ej * 8 + (nbd == 1 ? 1 : nbd == 2 ? 2 : 4)) {                                                           \
-        case 9: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 1, NORM>);                 \
-        case 10: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 2, NORM>);                \
-        case 12: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 4, NORM>);                \
-        case 17: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 1, NORM>);                \
-        case 18: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 2, NORM>);                \
-        case 20: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 4, NORM>);                \
-        case 33: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 1, NORM>);                \
-        case 34: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 2, NORM>);                \
-        default: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 4, NORM>);               \
+        case 9: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 1, NORM, false>);          \
+        case 10: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 2, NORM, false>);         \
+        case 12: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 1, 4, NORM, false>);         \
+        case 17: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 1, NORM, false>);         \
+        case 18: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 2, NORM, false>);         \
+        case 20: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 2, 4, NORM, false>);         \
+        case 33: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 1, NORM, false>);         \
+        case 34: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 2, NORM, false>);         \
+        default: return reinterpret_cast<const void*>(&k_moe_decode<WL_TYPE_Q4_K, DN, 4, 4, NORM, false>);        \
     }
     if (L.down_type == WL_TYPE_Q4_K) {
         if (norm) {
@@ -675,7 +776,18 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
         a.next_sh_gate_up = static_cast<const uint8_t*>(nx->shared_gate_up);
         a.next_sh_down = static_cast<const uint8_t*>(nx->shared_down);
         a.next_norm_w = (nx->flags & WL_MOE_PRE_NORM) ? nx->norm_weight : nullptr;
+        if (guess_instance(L) && (nx->flags & WL_MOE_PRE_NORM)) {
+            a.guess_router = nx->router;
+            a.guess_bias = nx->router_bias;
+            a.guess_norm_w = nx->norm_weight;
+            a.guess_eps = nx->norm_eps;
+        }
     }
+    // a guessing call also reads the guess the previous call may have left for it, in its last wavefront when
+    // that one has no phase A task
+    const int n_a =
+        L.n_experts + ((L.shared_gate_up && L.shared_gate) ? 1 : 0) + (L.shared_gate_up ? L.shared_inter : 0);
+    a.consume_guess = guess_instance(L) && n_a <= (kFusedWaves - 1) * a.G ? 1 : 0;
     void* args[] = {&a};
     const hipError_t e = hipLaunchKernel(kernel, dim3(static_cast<unsigned>(a.G)), dim3(kFusedThreads), args, 0, s);
     return e == hipSuccess ? WL_OK : static_cast<int>(e);

@@ -21,6 +21,7 @@ MAX_TOKENS = 8  # F.linear on a GGMLWeight runs the GEMV kernel up to this many 
 MAX_BATCH_EXPERTS = 64
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MOE_NO_FUSED, MOE_NO_MFMA, MOE_FORCE_MFMA, MOE_TEST_STARVE, MOE_PRE_NORM, MOE_RESIDUAL = 1, 2, 4, 8, 16, 32
+MOE_GUESS_NEXT = 64
 ESYNC = -10  # wl_moe_workspace_status: a bounded wait gave up
 EINVAL_SCOPE = -12  # wl_moe_fork_begin / wl_moe_fork_end used outside their pairing
 NOALLOC_SCRATCH_BYTES = 16 << 20  # WL_NOALLOC_SCRATCH_BYTES

@@ -7,8 +7,8 @@ import ctypes
 
 import torch
 
-from . import (MOE_FORCE_MFMA, MOE_NO_FUSED, MOE_NO_MFMA, MOE_PRE_NORM, MOE_RESIDUAL, TYPE_IDS, WlMoeLayer, _on_gpu,
-               _stream, _type_id, check, library, row_bytes)
+from . import (MOE_FORCE_MFMA, MOE_GUESS_NEXT, MOE_NO_FUSED, MOE_NO_MFMA, MOE_PRE_NORM, MOE_RESIDUAL, TYPE_IDS,
+               WlMoeLayer, _on_gpu, _stream, _type_id, check, library, row_bytes)
 
 
 def _ptr(t):
@@ -118,12 +118,20 @@ class MoELayer:
         check(library().wl_moe_check(ctypes.byref(s)))
         return other
 
-    def set_next(self, layer: "MoELayer" = None):
+    def set_next(self, layer: "MoELayer" = None, guess: bool = False):
         """The layer the caller runs after this one (or None). With the same shapes, a batch-1 call pulls the rows
         that layer reads before its routing is known (router, shared expert) into the GPU's caches while this
-        layer waits on its exchanges (WlMoeLayer.next). `layer` is kept alive by this one."""
+        layer waits on its exchanges (WlMoeLayer.next). `layer` is kept alive by this one.
+        guess: the caller runs `layer` on an input derived from this call's (the decoder loop, both layers with
+        pre_norm): a batch-1 call then also guesses that layer's experts, the top-k of its router on its RMSNorm
+        of this call's x, and pulls their gate_up rows into the caches (guess_next_layer's early read,
+        engines/base.py:392-406,472-474). Results are the same either way."""
         self._next = layer
         self.struct.next = None if layer is None else ctypes.addressof(layer.struct)
+        if guess and layer is not None:
+            self.struct.flags |= MOE_GUESS_NEXT
+        else:
+            self.struct.flags &= ~MOE_GUESS_NEXT
         check(library().wl_moe_check(ctypes.byref(self.struct)))
 
     def workspace_bytes(self, tokens: int) -> int:
