@@ -122,7 +122,12 @@ typedef struct WlMoeLayer {
      * x_i * inv * (1 + w_i) (rounded after each product; w = 0 when norm_weight is NULL). */
     const float* norm_weight;    /* fp32 [hidden] (post_attention_layernorm.weight) or NULL */
     float norm_eps;
-    int32_t reserved2;           /* 0 */
+    /* Routed experts whose routing weight is below this are skipped (0 = off): each token keeps its top expert,
+     * the others below the threshold are dropped (their ids read -1, their weights 0) and the kept weights are
+     * scaled by sum(all k weights) / sum(kept weights), both sums in pick order, so they add up to what the k did:
+     * Engine.skip_small_experts (engines/base.py:413-430), applied in the layer as Engine.moe applies it
+     * (:463-464), so dropped experts' weights are never read. wl_moe_route returns the routing without it. */
+    float min_expert_weight;
 } WlMoeLayer;
 
 #define WL_MOE_NO_FUSED 1        /* flags: never take the fused single-kernel decode path */

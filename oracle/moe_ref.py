@@ -37,6 +37,25 @@ def route(logits: np.ndarray, top_k: int, normalize: bool):
     return weights.astype(np.float32), ids
 
 
+def skip_small(weights: np.ndarray, ids: np.ndarray, min_weight: float):
+    """engines/base.py:413-430 (Engine.skip_small_experts) on route()'s output, columns in pick order (largest weight
+    first): keep = weight >= min_weight, and column 0 always; kept weights are scaled by S / K (S the sum of the k
+    weights, K of the kept ones, each added left to right in pick order in float32; torch's .sum order is not
+    specified, this is the order the kernels use); dropped columns get weight 0 and id -1. Returns (weights, ids)."""
+    w = np.asarray(weights, dtype=np.float32)
+    keep = w >= np.float32(min_weight)
+    keep[:, 0] = True
+    kept = np.where(keep, w, np.float32(0.0)).astype(np.float32)
+    S = w[:, 0].copy()
+    K = kept[:, 0].copy()
+    for i in range(1, w.shape[1]):
+        S = (S + w[:, i]).astype(np.float32)
+        K = (K + kept[:, i]).astype(np.float32)
+    scale = (S / K).astype(np.float32)
+    out = np.where(keep, (kept * scale[:, None]).astype(np.float32), np.float32(0.0)).astype(np.float32)
+    return out, np.where(keep, ids, -1).astype(np.int32)
+
+
 def silu(v: np.ndarray) -> np.ndarray:
     with np.errstate(over="ignore"):  # exp(-v) -> inf for very negative v gives silu = -0, as on the GPU
         return v / (1 + np.exp(-v))
@@ -83,7 +102,7 @@ def swiglu_hidden(x: np.ndarray, gate_up_w: np.ndarray, inter: int, dtype=np.flo
 
 
 def layer(x: np.ndarray, lw: dict, dtype=np.float32, chain: str = "fp32", return_routing: bool = False,
-          shared_chain: str = None, counts=None, layer_tokens: int = None):
+          shared_chain: str = None, counts=None, layer_tokens: int = None, min_expert_weight: float = 0.0):
     """The whole MoE layer for x fp32 [T, hidden]; lw is a layer dict as synth.moe_layer builds it. Returns
     y [T, hidden] (in dtype), and with return_routing also (ids, weights, shared gate values).
 
@@ -94,7 +113,8 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, chain: str = "fp32", return
     the shared expert's (e.g. "fp32" for dense fp32 shared weights run by torch). The weighted sum over experts is
     fp32, in ascending expert order. For x a sample of a larger call's tokens, counts ([n_experts], each expert's
     tokens in the whole call) and layer_tokens (the call's token count) let "split" place the experts as that
-    call does."""
+    call does. min_expert_weight > 0: skip_small on the routing first, as Engine.moe applies it
+    (engines/base.py:463-464); dropped picks (id -1) run no expert, and an expert's token count is its kept pairs."""
     if chain not in CHAINS:
         raise ValueError(f"chain must be one of {CHAINS}, not {chain!r}")
 
@@ -107,8 +127,10 @@ def layer(x: np.ndarray, lw: dict, dtype=np.float32, chain: str = "fp32", return
     x = np.ascontiguousarray(x, dtype=np.float32)
     logits = cref.router_logits(x, lw["router"], lw.get("router_bias"))
     weights, ids = route(logits, lw["top_k"], lw["norm_topk_prob"])
+    if min_expert_weight > 0:
+        weights, ids = skip_small(weights, ids, min_expert_weight)
     y = np.zeros((x.shape[0], hidden), dtype=dtype)
-    for expert in np.unique(ids):  # ascending, like each_expert's sorted combine (engines/base.py:580-589)
+    for expert in np.unique(ids[ids >= 0]):  # ascending, like each_expert's sorted combine (engines/base.py:580-589)
         token_idx, slot = np.nonzero(ids == expert)
         gate_up_w = dequantize_matrix(lw["gate_up"][expert], lw["gate_up_type"], 2 * inter, hidden)
         down_w = dequantize_matrix(lw["down"][expert], lw["down_type"], hidden, inter)

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout():
     assert hip.library().wl_abi_version() >> 16 == 1
-    # 7 weight pointers, 2 shared-expert pointers, 12 int32 fields, next, norm_weight, norm_eps + reserved2
+    # 7 weight pointers, 2 shared-expert pointers, 12 int32 fields, next, norm_weight, norm_eps + min_expert_weight
     assert ctypes.sizeof(hip.WlMoeLayer) == 7 * 8 + 2 * 8 + 12 * 4 + 8 + 8 + 8 == 144
 
 
@@ -108,6 +108,11 @@ def layer_struct(**over):
     ({"gate_up": FAKE + 4}, -4),
     ({"shared_gate_up": FAKE}, -3),  # shared gate_up without shared down
     ({"shared_gate_up": FAKE, "shared_down": FAKE, "shared_inter": 100}, -2),
+    ({"min_expert_weight": 0.05}, 0),
+    ({"min_expert_weight": 1.0}, 0),
+    ({"min_expert_weight": -0.1}, -2),
+    ({"min_expert_weight": 1.5}, -2),
+    ({"min_expert_weight": float("nan")}, -2),
 ])
 def test_layer_validation(over, code):
     lib = hip.library()

@@ -96,6 +96,63 @@ def test_fused_matches_multi_kernel(hip, c2, layer_c2):
         assert moe_ref.rel_err(y_f, y_m) < 1e-5
 
 
+@pytest.mark.parametrize("case", ["tie16", "tie_boundary", "nan_row"])
+def test_topk_ties_and_nan(hip, case):
+    """Selection on exactly tied and NaN logits, for the fused kernel's top-k (one token) and the multi-kernel path's
+    (wave_topk): ties go to the lower expert id, NaN ranks as -inf, as the oracle's route does (engines/base.py:91-97
+    with a fixed tie rule). tie16: 16 experts share the largest logit, 8 are picked; tie_boundary: 3 experts tie
+    across the 8th/9th place; nan_row: one router row is NaN."""
+    lw = dict(synth.moe_layer(31, experts=64, top_k=8))
+    router = lw["router"].copy()
+    x = synth.tokens(32, 1)
+    base = cref.router_logits(x, router)[0]
+    order = np.argsort(-base, kind="stable")
+    if case == "tie16":
+        router[order[:16]] = router[order[0]]  # 16 identical rows: identical logits, the largest
+    elif case == "tie_boundary":
+        router[order[7:10]] = router[order[7]]  # the 8th, 9th and 10th tie
+    else:
+        router[order[0]] = np.nan  # the would-be top expert
+    lw["router"] = router
+    logits = cref.router_logits(x, router)
+    _, ids_ref = moe_ref.route(logits, 8, True)
+    for fused in (True, False):
+        layer = hip.MoELayer.from_host(lw, fused=fused)
+        assert layer.plan(1) == ("fused" if fused else "gemv")
+        print(f"[moe] topk {case} fused={fused}", flush=True)
+        y, ids, wts = run_layer(hip, layer, x)
+        np.testing.assert_array_equal(ids, ids_ref)
+        assert np.isfinite(y).all()  # a NaN logit ranks and weighs as -inf: no NaN reaches the output
+
+
+@pytest.mark.parametrize("T,fused", [(1, True), (1, False), (9, True), (64, True), (300, True)])
+def test_skip_small_experts(hip, layer_c2, T, fused):
+    """min_expert_weight (Engine.skip_small_experts, engines/base.py:413-430, applied in Engine.moe at :463-464):
+    the layer's ids and weights equal the oracle's skip_small of its routing (a dropped pick has id -1 and weight 0,
+    the kept weights are scaled back to the sum of the k) and its output the oracle's layer on the kept experts
+    only, each expert placed by its kept tokens. One token in the fused kernel and on the multi-kernel path, 9 and
+    64 tokens (top-k over the router's partials, split plan), 300 tokens (two grouping chunks)."""
+    thr = 0.12
+    layer = hip.MoELayer.from_host(layer_c2, fused=fused, min_expert_weight=thr)
+    x = synth.tokens(400 + T, T)
+    plan = layer.plan(T)
+    chain = "split" if plan in ("split", "mfma") else "fp32"
+    print(f"[moe] skip_small T={T} plan={plan}", flush=True)
+    y, ids, wts = run_layer(hip, layer, x)
+    y_ref, ids_ref, wts_ref, _ = moe_ref.layer(x, layer_c2, chain=chain, return_routing=True,
+                                               dtype=np.float64 if chain == "split" else np.float32,
+                                               min_expert_weight=thr)
+    np.testing.assert_array_equal(ids, ids_ref)
+    np.testing.assert_allclose(wts, wts_ref, rtol=4e-6, atol=1e-7)
+    assert (ids == -1).any() and (ids[:, 0] >= 0).all()  # some picks dropped, never a token's top one
+    err = moe_ref.rel_err(y, y_ref)
+    print(f"[moe] skip_small T={T}: rel err {err:.2e}", flush=True)
+    assert err < TOL
+    # the routing call (route(), engines/base.py:91-97) is unaffected by the threshold
+    w_r, ids_r, _, _ = layer.route(torch.from_numpy(x).cuda(), return_logits=True)
+    assert (ids_r.cpu().numpy() >= 0).all()
+
+
 def test_fused_back_to_back(hip, c2, layer_c2):
     """Many fused calls in a row on one workspace (the grid barrier's words must reset each time), checked
     against the oracle at the end."""

@@ -236,3 +236,58 @@ def test_topk_margins():
     logits = np.array([[5, 4, 3, 2, 1, 0], [1, 1, 1, 1, 1, 1], [0, 3, 9, 3, 2, 8]], dtype=np.float32)
     np.testing.assert_array_equal(moe_ref.topk_margins(logits, 2), [1, 0, 5])
     np.testing.assert_array_equal(moe_ref.topk_margins(logits, 3), [1, 0, 0])
+
+
+def test_skip_small_closed_forms():
+    """moe_ref.skip_small (engines/base.py:413-430) on cases whose answer is fixed by the definition: the kept
+    weights keep their ratios and add up to the sum of all k (a scale of K / S or an S without the dropped ones
+    fails); a weight equal to the threshold is kept (>=); the top pick is kept when everything is below; nothing
+    dropped leaves the routing bit for bit unchanged."""
+    ids = np.array([[7, 3, 9, 1]], dtype=np.int32)
+    w = np.array([[0.5, 0.25, 0.125, 0.125]], dtype=np.float32)
+    out, oid = moe_ref.skip_small(w, ids, 0.2)
+    np.testing.assert_array_equal(oid, [[7, 3, -1, -1]])
+    assert out[0, 2] == 0.0 and out[0, 3] == 0.0
+    assert out[0, 0] == 2 * out[0, 1]  # one scale for both: the ratio of two powers of 2 stays exact
+    assert abs(float(out[0, 0]) + float(out[0, 1]) - 1.0) <= 2 ** -23  # S = 1, not K = 0.75
+    assert out[0, 0] > 0.5  # scaled up, by S / K = 4 / 3
+    # equal to the threshold: kept
+    w2 = np.array([[0.5, 0.25, 0.25]], dtype=np.float32)
+    out2, oid2 = moe_ref.skip_small(w2, ids[:, :3], 0.25)
+    np.testing.assert_array_equal(oid2, ids[:, :3])
+    np.testing.assert_array_equal(out2, w2)
+    # all below: the top pick alone, carrying the whole sum
+    w3 = np.array([[0.3, 0.3, 0.2, 0.2]], dtype=np.float32)
+    out3, oid3 = moe_ref.skip_small(w3, ids, 0.9)
+    np.testing.assert_array_equal(oid3, [[7, -1, -1, -1]])
+    assert abs(float(out3[0, 0]) - 1.0) <= 2 ** -23 and (out3[0, 1:] == 0).all()
+    # nothing dropped: unchanged bit for bit (K == S, scale exactly 1)
+    logits = np.random.default_rng(3).standard_normal((50, 64)).astype(np.float32)
+    wr, ir = moe_ref.route(logits, 8, True)
+    out4, oid4 = moe_ref.skip_small(wr, ir, 1e-12)
+    np.testing.assert_array_equal(out4.view(np.uint32), wr.view(np.uint32))
+    np.testing.assert_array_equal(oid4, ir)
+
+
+def test_layer_skip_small_experts():
+    """layer(min_expert_weight): a threshold no weight reaches equals the layer with each token's top expert alone at
+    the weight sum of its k (here 1, renormalized), built from the oracle's own expert_ffn; a threshold every weight
+    passes equals the plain layer bit for bit."""
+    lw = synth.moe_layer(21, experts=16, top_k=4)
+    x = synth.tokens(22, 5)
+    plain = moe_ref.layer(x, lw)
+    np.testing.assert_array_equal(moe_ref.layer(x, lw, min_expert_weight=1e-12), plain)
+    y, ids, wts, sg = moe_ref.layer(x, lw, min_expert_weight=1.0, return_routing=True)
+    assert (ids[:, 1:] == -1).all() and (wts[:, 1:] == 0).all()
+    _, ids_full = moe_ref.route(cref.router_logits(x, lw["router"], lw.get("router_bias")), 4, True)
+    np.testing.assert_array_equal(ids[:, 0], ids_full[:, 0])
+    inter, hidden = lw["inter"], lw["hidden"]
+    want = np.zeros_like(plain)
+    for t in range(x.shape[0]):
+        e = ids[t, 0]
+        gu = q.dequantize_matrix(lw["gate_up"][e], lw["gate_up_type"], 2 * inter, hidden)
+        dn = q.dequantize_matrix(lw["down"][e], lw["down_type"], hidden, inter)
+        want[t] = moe_ref.expert_ffn(x[t:t + 1], gu, dn, inter)[0] * wts[t, 0]
+    # the shared expert's part alone: the same layer with every routed expert's blocks zero (they dequantize to 0)
+    sh = moe_ref.layer(x, dict(lw, gate_up=np.zeros_like(lw["gate_up"]), down=np.zeros_like(lw["down"])))
+    np.testing.assert_allclose(y - sh, want, rtol=1e-5, atol=1e-5 * float(np.abs(want).max()))

@@ -167,11 +167,11 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, c
 
 // ---------------------------------------------------------------------------------------------------------------
 // Top-k: one wavefront per token (wave_topk). corder[t, i] = the slot of the token's i-th smallest expert id, the
-// order the combine adds experts in.
+// order the combine adds experts in. min_w > 0: the layer's skip_small_experts (skip_small; dropped picks id -1).
 template <int EJ>
 __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, int T, int E, int k, int renorm,
                                               int32_t* __restrict__ ids, float* __restrict__ wts,
-                                              int32_t* __restrict__ corder) {
+                                              int32_t* __restrict__ corder, float min_w) {
     __shared__ uint32_t scratch[4][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
@@ -179,6 +179,7 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, 
     int id, id_rank;
     float w;
     wave_topk<EJ>(logits + static_cast<int64_t>(t) * E, E, k, renorm != 0, scratch[wv], lane, id, w, id_rank);
+    if (min_w > 0.0f) skip_small(w, id, k, min_w, lane);
     if (lane < k) {
         ids[static_cast<int64_t>(t) * k + lane] = id;
         wts[static_cast<int64_t>(t) * k + lane] = w;
@@ -269,7 +270,7 @@ template <int EJ, int NSEG>
 __device__ __forceinline__ void topk_parts(const float* __restrict__ parts, int nseg, const float* __restrict__ bias,
                                            int T, int E, int rows, int k, int renorm, int32_t* __restrict__ ids,
                                            float* __restrict__ wts, int32_t* __restrict__ corder,
-                                           float* __restrict__ sg) {
+                                           float* __restrict__ sg, float min_w) {
     __shared__ float lg[64 * EJ];
     __shared__ uint32_t scratch[64];
     const int t = blockIdx.x;
@@ -299,6 +300,7 @@ __device__ __forceinline__ void topk_parts(const float* __restrict__ parts, int 
         int id, id_rank;
         float wsel;
         wave_topk<EJ>(lg, E, k, renorm != 0, scratch, lane, id, wsel, id_rank);
+        if (min_w > 0.0f) skip_small(wsel, id, k, min_w, lane);
         if (lane < k) {
             ids[static_cast<int64_t>(t) * k + lane] = id;
             wts[static_cast<int64_t>(t) * k + lane] = wsel;
@@ -311,8 +313,9 @@ template <int EJ, int NSEG>
 __global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ parts, int nseg,
                                                      const float* __restrict__ bias, int T, int E, int rows, int k,
                                                      int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                     int32_t* __restrict__ corder, float* __restrict__ sg) {
-    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg);
+                                                     int32_t* __restrict__ corder, float* __restrict__ sg,
+                                                     float min_w) {
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg, min_w);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -320,7 +323,8 @@ __global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ p
 // Within a chunk of kSortChunk tokens, bit t of row e of an LDS bitmap says token t picked expert e; a pair's rank
 // among its expert's pairs is the popcount of the bits before it, so the result is deterministic and stable
 // (pairs of one expert stay in token order). Outputs:
-//   offsets[E+1]    first sorted position of each expert's pairs; offsets[E] = T*k
+//   offsets[E+1]    first sorted position of each expert's pairs; offsets[E] = the pairs grouped (T*k less
+//                   the picks skip_small dropped, whose pair_pos is -1)
 //   active[0]       number of experts with at least one pair; active[1..] those experts, ascending
 //   sorted[P]       pair id (t*k + slot) at each sorted position;  pair_pos[P] the inverse
 // One chunk: k_sort_small. Many chunks: k_sort_hist (per-chunk bitmaps, counts and ranks) -> k_sort_scan (chunk
@@ -395,7 +399,10 @@ __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict_
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= static_cast<int64_t>(T) * k) return;
     const int e = ids[p];
-    if (e < 0 || e >= E) return;
+    if (e < 0 || e >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
+        pair_pos[p] = -1;
+        return;
+    }
     const int c = static_cast<int>(p / k) / kSortChunk;
     const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
     const bool bf16 = offsets[e + 1] - offsets[e] > flag_above;
@@ -545,13 +552,16 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
         offsets[e] = off;
         lds_off[e] = static_cast<uint32_t>(off) | (big ? kPosBf16 : 0u);
     }
-    if (tid == 0) offsets[E] = P;
+    if (tid == 0) offsets[E] = total;  // the pairs grouped: T k less any skip_small dropped
     const int apos = block_scan_excl((c > 0 && !big) ? 1 : 0, wsum, &total);  // its barriers also publish lds_off
     if (e < E && c > 0 && !big) active[1 + apos] = e;
     if (tid == 0) active[0] = total;
     for (int q = tid; q < P; q += blockDim.x) {
         const int ex = lds_ids[q];
-        if (ex < 0 || ex >= E) continue;
+        if (ex < 0 || ex >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
+            pair_pos[q] = -1;
+            continue;
+        }
         const uint32_t o = lds_off[ex];
         const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
         sorted[pos] = q;
@@ -596,9 +606,9 @@ __global__ __launch_bounds__(1024) void k_topk_group(const float* __restrict__ p
                                                      const float* __restrict__ bias, int T, int E, int rows, int k,
                                                      int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
                                                      int32_t* __restrict__ corder, float* __restrict__ sg,
-                                                     GroupOut g) {
+                                                     GroupOut g, float min_w) {
     __shared__ int last;
-    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg);
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg, min_w);
     __syncthreads();  // the picks are stored by wavefront 0, whose thread 0 counts the workgroup done
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -645,7 +655,7 @@ __global__ __launch_bounds__(kSortSmallThreads) void k_sort_scan(int T, int k, i
     int total;
     const int off = block_scan_excl(c, wsum, &total);
     if (mine) offsets[e] = off;
-    if (threadIdx.x == 0) offsets[E] = T * k;
+    if (threadIdx.x == 0) offsets[E] = total;  // the pairs grouped: T k less any skip_small dropped
     if (mine) {
         if (nchunks <= kScanBatch) {
 #pragma unroll
@@ -1273,6 +1283,7 @@ static int check_one_layer(const WlMoeLayer* L) {
     if (!L) return WL_EINVAL_NULL;
     if ((L->flags & WL_MOE_PRE_NORM) && (!(L->norm_eps >= 0.0f) || reinterpret_cast<uintptr_t>(L->norm_weight) % 16))
         return WL_EINVAL_SHAPE;
+    if (!(L->min_expert_weight >= 0.0f && L->min_expert_weight <= 1.0f)) return WL_EINVAL_SHAPE;  // NaN too
     if (!L->gate_up || !L->down || !L->router) return WL_EINVAL_NULL;
     if (block_bytes(L->gate_up_type) < 0 || block_bytes(L->down_type) < 0) return WL_EINVAL_TYPE;
     if (L->hidden <= 0 || L->hidden % kQK != 0 || L->hidden > kRouterSeg * 32 * kRouterMaxJ) return WL_EINVAL_SHAPE;
@@ -1316,19 +1327,19 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
 }
 
 static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int32_t* ids, float* wts,
-                       int32_t* corder, hipStream_t s) {
+                       int32_t* corder, float min_w, hipStream_t s) {
     const int grid = static_cast<int>((T + 3) / 4);
     const int E = L.n_experts, k = L.top_k, rn = L.norm_topk_prob ? 1 : 0, Ti = static_cast<int>(T);
     if (E <= 64)
-        k_topk<1><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+        k_topk<1><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
     else if (E <= 128)
-        k_topk<2><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+        k_topk<2><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
     else if (E <= 256)
-        k_topk<4><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+        k_topk<4><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
     else if (E <= 512)
-        k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+        k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
     else
-        k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder);
+        k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
     return launch_status();
 }
 
@@ -1363,7 +1374,7 @@ static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w,
         };
         auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
         kernel<<<grid, kSortSmallThreads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts,
-                                                  w.corder, sg, *g);
+                                                  w.corder, sg, *g, L.min_expert_weight);
         return launch_status();
     }
     auto pick = [&](auto seg32) {
@@ -1372,7 +1383,8 @@ static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w,
                : E <= 512 ? k_topk_parts<8, S> : k_topk_parts<16, S>;
     };
     auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
-    kernel<<<grid, threads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts, w.corder, sg);
+    kernel<<<grid, threads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts, w.corder, sg,
+                                    L.min_expert_weight);
     return launch_status();
 }
 
@@ -1553,7 +1565,7 @@ const char* wl_error_string(int code) {
     return "unknown error";
 }
 
-int wl_abi_version(void) { return (1 << 16) | 2; }  // 1.2: WlMoeLayer.next, wl_moe_layer_noalloc, status
+int wl_abi_version(void) { return (1 << 16) | 3; }  // 1.3: min_expert_weight (was reserved2, 0); 1.2: next, noalloc
 
 int wl_moe_check(const WlMoeLayer* layer) { return check_layer(layer); }
 
@@ -1574,7 +1586,7 @@ int wl_moe_route(const WlMoeLayer* layer, const float* x, int64_t tokens, float*
     rc = tokens >= kTiledRouterMinTokens ? launch_router_tiled(*layer, x, tokens, logits, shared_gate_out, nullptr, s)
                                          : launch_router(*layer, x, tokens, logits, shared_gate_out, nullptr, s);
     if (rc) return rc;
-    return launch_topk(*layer, logits, tokens, ids, weights, nullptr, s);
+    return launch_topk(*layer, logits, tokens, ids, weights, nullptr, 0.0f, s);  // route(): no skipping
 }
 
 
@@ -1712,7 +1724,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
                  : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
         if (rc) return rc;
         mark(1);
-        rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, s);
+        rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, L.min_expert_weight, s);
         if (rc) return rc;
         mark(2);
     }

@@ -176,6 +176,41 @@ __device__ __forceinline__ float pick_weight(float my_v, float m, float s, int k
     return renorm ? p / wsum : p;
 }
 
+// Engine.skip_small_experts (engines/base.py:413-430) on one token's picks, lane r < k holding pick r (largest
+// weight first) with weight w and expert id: a pick is kept when its weight is at least min_w, and pick 0 always;
+// the kept weights are scaled by S / K, S the sum of the k weights and K of the kept ones (each added in pick
+// order); a dropped pick gets id -1 and weight 0. Returns whether lane's pick is kept. Call with the whole
+// wavefront; min_w > 0.
+__device__ __forceinline__ bool skip_small(float& w, int& id, int k, float min_w, int lane) {
+    const bool keep = lane < k && (lane == 0 || w >= min_w);
+    const float kw = keep ? w : 0.0f;
+    float S = 0.0f, K = 0.0f;
+    for (int r0 = 0; r0 < k; r0 += 8) {
+        float pr[8], kr[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            pr[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (r0 + i) & 63));
+            kr[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, kw), (r0 + i) & 63));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (r0 + i < k) {
+                S = r0 + i == 0 ? pr[i] : S + pr[i];
+                K = r0 + i == 0 ? kr[i] : K + kr[i];
+            }
+    }
+    const float scale = S / K;
+    if (lane < k) {
+        if (keep) {
+            w = w * scale;
+        } else {
+            w = 0.0f;
+            id = -1;
+        }
+    }
+    return keep;
+}
+
 // max(v, the value of the lane DPP control CTRL selects) on unsigned 32-bit values, every lane sourcing
 __device__ __forceinline__ int umax_dpp_impl(int v, int o) {
     return static_cast<int>(max(static_cast<uint32_t>(v), static_cast<uint32_t>(o)));

@@ -79,6 +79,7 @@ struct FusedArgs {
     const float* norm_w;  // NORM: the RMSNorm weight (zero-centered) or NULL
     float norm_eps;
     int residual;         // y = x + MoE
+    float min_w;          // > 0: skip_small_experts with this threshold (the picks kept are the experts run)
     // the next-layer guess (NORM only). Producer (guess_router non-NULL): the next layer's router (and bias) on this
     // layer's x normalized with the next layer's RMSNorm (weight or NULL, eps), one row per workgroup while it waits
     // for h, left in the workspace. Consumer (consume_guess): the previous call's guess on this workspace, read
@@ -187,6 +188,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
+    __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
     __shared__ __attribute__((aligned(16))) float lds_xn[NORM ? kFusedMaxHidden : 4];  // NORM: the normalized x
     // GUESS (the next-layer guess): x normalized with the next layer's RMSNorm; the previous call's guess (ids)
     __shared__ __attribute__((aligned(16))) float lds_xg[GUESS ? kFusedMaxHidden : 4];
@@ -469,15 +471,44 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         lane_sync();
         // the picks in ascending id order for the tasks; the weights (needed only by the final sum) come later
         const int my_id = lane < k ? lds_pick[lane] : 0;
-        int idr[kFusedMaxK];
+        if (a.min_w > 0.0f) {
+            // skip_small_experts: which picks run depends on the weights, so they are computed here, before any
+            // gate_up load (the same arithmetic as below); only the kept picks become tasks
+            const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
+            const float m = lv0 == lv0 ? lv0 : -INFINITY;
+            const float ssum = softmax_sum<EJ>(lds_logits, E, lane, m);
+            const float lv = lds_logits[my_id];
+            float my_w = pick_weight(lane < k ? (lv == lv ? lv : -INFINITY) : -INFINITY, m, ssum, k, a.renorm != 0,
+                                     lane);
+            int out_id = my_id;
+            const bool keep = skip_small(my_w, out_id, k, a.min_w, lane);
+            const uint64_t kept = __ballot(keep);
+            int my_rank = 0;  // position among the kept ids in ascending order
 #pragma unroll
-        for (int q = 0; q < kFusedMaxK; q++) idr[q] = __builtin_amdgcn_readlane(my_id, q);
-        int my_rank = 0;  // position among the k ids in ascending order
+            for (int q = 0; q < kFusedMaxK; q++)
+                my_rank += (((kept >> q) & 1u) && __builtin_amdgcn_readlane(my_id, q) < my_id) ? 1 : 0;
+            if (keep) {
+                lds_sel[my_rank] = my_id;
+                lds_wsel[my_rank] = my_w;
+            }
+            if (lane < k && b == 0) {
+                if (a.ids_out) a.ids_out[lane] = out_id;
+                if (a.wts_out) a.wts_out[lane] = my_w;
+            }
+            if (lane == 0) lds_kk = __popcll(kept);
+        } else {
+            int idr[kFusedMaxK];
 #pragma unroll
-        for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && idr[q] < my_id) ? 1 : 0;
-        if (lane < k) lds_sel[my_rank] = my_id;
+            for (int q = 0; q < kFusedMaxK; q++) idr[q] = __builtin_amdgcn_readlane(my_id, q);
+            int my_rank = 0;  // position among the k ids in ascending order
+#pragma unroll
+            for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && idr[q] < my_id) ? 1 : 0;
+            if (lane < k) lds_sel[my_rank] = my_id;
+            if (lane == 0) lds_kk = k;
+        }
     }
     __syncthreads();
+    const int kk = lds_kk;  // the experts run (k unless skip_small dropped some)
     int sel[kFusedMaxK];
 #pragma unroll
     for (int s = 0; s < kFusedMaxK; s++) sel[s] = lds_sel[s];
@@ -490,7 +521,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     };
 
     // phase B: every load of this wavefront's gate_up tasks (at most kGateUpTasks), before any arithmetic
-    const int n_tasks = k * I;
+    const int n_tasks = kk * I;
     RawLane<GU> graw[kGateUpTasks][2];
 #pragma unroll
     for (int q = 0; q < kGateUpTasks; q++) {
@@ -504,7 +535,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     }
     // the routing weights, needed only by the final sum: wavefront 0 computes them while the loads above are in flight
     // (softmax over all logits with the max from pick 0, as softmax_stats takes it; renormalised in pick order)
-    if (wv == 0) {
+    if (wv == 0 && !(a.min_w > 0.0f)) {
         const int my_id = lane < k ? lds_pick[lane] : 0;
         const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
         const float m = lv0 == lv0 ? lv0 : -INFINITY;
@@ -594,8 +625,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                            a.guess_bias ? __fadd_rn(total, a.guess_bias[e]) : total);
         }
     };
-    if (guess && wv == guess_wave && !(owner && wv < k)) guess_rows();
-    if (owner && wv < k) {
+    if (guess && wv == guess_wave && !(owner && wv < kk)) guess_rows();
+    if (owner && wv < kk) {
         auto own_row = [&](int pass) { return kOwnRows * b + R * pass + drow; };
         RawLane<DN> draw[NBD];
         const uint8_t* w = a.down + static_cast<int64_t>(expert_of(wv)) * a.down_stride;
@@ -627,7 +658,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     if (owner && threadIdx.x < kOwnRows) {
         const int r = threadIdx.x;
         float acc = 0.0f;
-        for (int s = 0; s < k; s++)
+        for (int s = 0; s < kk; s++)
             acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
         if (shared) acc = acc + sgv * lds_sh[r];
         if (a.residual) acc = __fadd_rn(a.x[kOwnRows * b + r], acc);
@@ -763,6 +794,7 @@ int launch_fused(const WlMoeLayer& L, const float* x, float* y, int32_t* ids, fl
     a.norm_w = L.norm_weight;
     a.norm_eps = L.norm_eps;
     a.residual = (L.flags & WL_MOE_RESIDUAL) ? 1 : 0;
+    a.min_w = L.min_expert_weight;
     const WlMoeLayer* nx = L.next;
     // the next layer's phase A maps tasks to workgroups and wavefronts the same way only with the same shapes
     if (nx && nx->hidden == L.hidden && nx->n_experts == L.n_experts && nx->inter == L.inter &&

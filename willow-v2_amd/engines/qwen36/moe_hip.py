@@ -93,11 +93,11 @@ class HipMoE:
                 raise HipError(ESYNC, f"layer {layer}: " + library().wl_error_string(ESYNC).decode())
 
     def moe(self, x: torch.Tensor, layer: int, residual: torch.Tensor = None) -> torch.Tensor:
-        if getattr(self, "min_expert_weight", 0.0):
-            # engines/base.py:413-430,463-464 (skip_small_experts): not run on this backend; refusing keeps a run
-            # with --min-expert-weight from silently computing every routed expert
-            raise NotImplementedError("min_expert_weight (skip_small_experts) is not supported by the HIP MoE layer")
         view, dense = self.hip_layer(layer)
+        min_w = float(getattr(self, "min_expert_weight", 0.0) or 0.0)
+        if view.min_expert_weight != min_w:
+            # Engine.skip_small_experts (engines/base.py:413-430), applied in the layer as Engine.moe does (:463-464)
+            view.set_min_expert_weight(min_w)
         nxt = layer + 1
         if getattr(view, "_next", None) is None and nxt < len(getattr(self.experts, "layers", ())):
             # the next layer's router and shared-expert rows are pulled into the caches during this layer

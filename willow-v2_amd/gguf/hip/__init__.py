@@ -48,7 +48,7 @@ class WlMoeLayer(ctypes.Structure):
         ("shared_inter", ctypes.c_int32), ("n_experts", ctypes.c_int32), ("top_k", ctypes.c_int32),
         ("norm_topk_prob", ctypes.c_int32), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32),
         ("next", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p), ("norm_eps", ctypes.c_float),
-        ("reserved2", ctypes.c_int32),
+        ("min_expert_weight", ctypes.c_float),
     ]
 
 

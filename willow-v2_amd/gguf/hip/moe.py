@@ -25,13 +25,16 @@ class MoELayer:
     Tensors may be views into a larger store; each expert's bytes must be contiguous (a row of a 2-D tensor).
     pre_norm: run on the zero-centered RMSNorm of x (norm_weight fp32 [hidden] or None for 0, norm_eps), as the
     model calls the layer on rms_norm(x) (engines/qwen36/model.py:22, engines/base.py:27-31); residual: return
-    x + MoE(...), the residual add of the same line."""
+    x + MoE(...), the residual add of the same line. min_expert_weight: Engine.skip_small_experts
+    (engines/base.py:413-430): routed experts below this routing weight are skipped (each token keeps its top one;
+    the kept weights are scaled back to the sum of the k), 0 = off."""
 
     def __init__(self, *, gate_up, down, router, hidden: int, inter: int, n_experts: int, top_k: int,
                  norm_topk_prob: bool = True, gate_up_type: str = "Q4_K", down_type: str = "Q6_K",
                  router_bias=None, shared_gate_up=None, shared_down=None, shared_gate=None, shared_inter=None,
                  shared_gate_up_type=None, shared_down_type=None, fused: bool = True, mfma: str = "auto",
-                 pre_norm: bool = False, norm_weight=None, norm_eps: float = 1e-6, residual: bool = False):
+                 pre_norm: bool = False, norm_weight=None, norm_eps: float = 1e-6, residual: bool = False,
+                 min_expert_weight: float = 0.0):
         for name, t in (("gate_up", gate_up), ("down", down), ("router", router)):
             _on_gpu(t, name)
         if router.dtype != torch.float32:
@@ -80,6 +83,8 @@ class MoELayer:
             s.norm_eps = float(norm_eps)
         if residual:
             s.flags |= MOE_RESIDUAL
+        s.min_expert_weight = float(min_expert_weight)
+        self.min_expert_weight = float(min_expert_weight)
         self.struct = s
         check(library().wl_moe_check(ctypes.byref(s)))
 
@@ -117,6 +122,12 @@ class MoELayer:
         other.struct = s
         check(library().wl_moe_check(ctypes.byref(s)))
         return other
+
+    def set_min_expert_weight(self, w: float):
+        """Engine.min_expert_weight for this layer's calls (0 = off); see the class docstring."""
+        self.struct.min_expert_weight = float(w)
+        check(library().wl_moe_check(ctypes.byref(self.struct)))
+        self.min_expert_weight = float(w)
 
     def set_next(self, layer: "MoELayer" = None, guess: bool = False):
         """The layer the caller runs after this one (or None). With the same shapes, a batch-1 call pulls the rows
