@@ -549,8 +549,10 @@ __device__ __forceinline__ void gemm_loop(uint8_t (&bufs)[2][tile_bytes<TILE>()]
     bf16x8 a0[kRT], a1[kRT], b[NT];
     const int nsteps = nitems * nblocks;
     for (int st = 0; st < nsteps; st++) {
-        wait_stage();     // this chunk's LDS tile has landed
-        __syncthreads();  // ... for every wavefront, and the other buffer is free
+        if (!(nblocks <= 2 && st >= nblocks)) {  // resident chunks: staged and waited for by step nblocks - 1
+            wait_stage();     // this chunk's LDS tile has landed
+            __syncthreads();  // ... for every wavefront, and the other buffer is free
+        }
         const int sn = st + 1 < nsteps ? st + 1 : st;
         const int in = sn / nblocks, kn = sn - in * nblocks;
 #pragma unroll
