@@ -545,6 +545,52 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
     if (e < E)
 #pragma unroll
         for (int wd = 0; wd < kSortWords; wd++) c += __popc(bits[kSortWords * e + wd]);
+    if (P <= 1024 && E <= 256 && T <= kDownTileTokens) {
+        // Few pairs (batched decode): every MFMA expert and the shared expert fit one tile of either list, so
+        // the four scans below (positions, GEMV experts, the two tile lists) are one scan of three packed counts:
+        // pairs in bits 0..10 (<= 1024), GEMV experts in 11..19 and MFMA experts in 20..28 (<= 256 each), whose
+        // prefix sums stay inside their fields. The same outputs, with 4 barriers instead of 13.
+        const bool big = to.tiles && c > to.gemv_max;  // an MFMA expert
+        const bool act = c > 0 && !big;                 // a GEMV expert
+        int total;
+        const int pre = block_scan_excl(c | (act ? 1 << 11 : 0) | (big ? 1 << 20 : 0), wsum, &total);
+        const int off = pre & 0x7FF, apos = (pre >> 11) & 0x1FF, tpos = pre >> 20;
+        const int n_big = total >> 20;
+        if (e < E) {
+            offsets[e] = off;
+            lds_off[e] = static_cast<uint32_t>(off) | (big ? kPosBf16 : 0u);
+            if (act) active[1 + apos] = e;
+            if (big) {
+                to.tiles[tpos] = make_int4(e, off, c, 0);
+                to.tiles_down[tpos] = make_int4(e, off, c, 0);
+            }
+        }
+        if (tid == 0) {
+            offsets[E] = total & 0x7FF;  // the pairs grouped: T k less any skip_small dropped
+            active[0] = (total >> 11) & 0x1FF;
+            if (to.tiles) {
+                if (to.with_shared) {
+                    to.tiles[n_big] = make_int4(E, 0, T, 0);
+                    to.tiles_down[n_big] = make_int4(E, 0, T, 0);
+                }
+                to.n_tiles[0] = to.n_tiles[1] = n_big + (to.with_shared ? 1 : 0);
+            }
+        }
+        __syncthreads();  // lds_off for every thread
+        for (int q = tid; q < P; q += blockDim.x) {
+            const int ex = lds_ids[q];
+            if (ex < 0 || ex >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
+                pair_pos[q] = -1;
+                continue;
+            }
+            const uint32_t o = lds_off[ex];
+            const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
+            sorted[pos] = q;
+            pair_pos[q] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (o & kPosBf16));
+        }
+        if (fork_sync) publish_grouping(fork_sync, withhold);
+        return;
+    }
     int total;
     const int off = block_scan_excl(c, wsum, &total);
     const bool big = to.tiles && c > to.gemv_max;  // an MFMA expert
