@@ -634,6 +634,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         for (int p = 0; p < NBD; p++)
             draw[p].fetch(w + static_cast<int64_t>(own_row(p)) * dn_rs + kb * BlockInfo<DN>::bytes, c);
         if (guess && wv == guess_wave) guess_rows();
+        // the down rows unpacked while h crosses workgroups (the first h poll waits for their loads anyway)
+        Lane32 wr[NBD];
+#pragma unroll
+        for (int p = 0; p < NBD; p++) draw[p].unpack(c, wr[p]);
         float* hs = lds_h[wv];
         ok = gather_tagged_wave<4 * NBD>(
                  a.sync, tag, a.spin_limit, [&](int i) { return kTagH + 2 * (wv * I + i); },
@@ -646,9 +650,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         const float shl = sum16(hl), shh = sum16(hh);
 #pragma unroll
         for (int p = 0; p < NBD; p++) {
-            Lane32 wr;
-            draw[p].unpack(c, wr);
-            const float v = group_sum<WIDTH>(lane_dot_s(wr, hl, hh, shl, shh));
+            const float v = group_sum<WIDTH>(lane_dot_s(wr[p], hl, hh, shl, shh));
             if ((lane % WIDTH) == 0) lds_p[wv * kOwnRows + R * p + drow] = v;
         }
     }
