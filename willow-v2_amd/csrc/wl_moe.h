@@ -76,7 +76,7 @@ constexpr int kDownSlabsMax = 4;            // prefill: most 256-row slabs per d
 // bf16 MFMA GEMMs: the reference applies the rule of gguf/metal.py:20,404-407 to each expert's own tokens
 // (engines/base.py:566-571).
 constexpr int kGemvMaxTokens = 8;
-constexpr uint32_t kPosBf16 = 0x80000000u;  // pair_pos flag: the pair's expert output is bf16 (an MFMA expert)
+constexpr uint32_t kPosBf16 = 0x80000000u;  // position flag: the pair's expert output is bf16 (an MFMA expert)
 constexpr int kTiledRouterMinTokens = 2048;  // router as a tiled kernel from this many tokens
 constexpr int kRouterPartsMaxT = 64;         // wl_moe_layer's router for 2 .. this many tokens: per-segment partials
 
@@ -111,13 +111,13 @@ struct Workspace {
     float* sg;          // [T]      sigmoid(shared gate)
     int32_t* ids;       // [T, k]
     float* wts;         // [T, k]
-    int32_t* corder;    // [T, k]   slots in ascending expert id
+    int32_t* crank;     // [T, k]   each slot's rank among the token's expert ids (ascending)
     int32_t* rank;      // [T*k]    rank of a pair within its chunk and expert
     int32_t* hist;      // [chunks, E]
     int32_t* offsets;   // [E+1]
     int32_t* active;    // [1+E]
     int32_t* sorted;    // [T*k]
-    int32_t* pair_pos;  // [T*k]
+    uint2* picks;       // [T, k]   the combine's table: (position | kPosBf16, weight bits) in ascending expert id
     float* h;           // [T*k, inter]   by sorted position
     float* o;           // [T*k, hidden]  by sorted position
     float* h_sh;        // [T, shared_inter]

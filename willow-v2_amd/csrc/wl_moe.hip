@@ -166,12 +166,13 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, c
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Top-k: one wavefront per token (wave_topk). corder[t, i] = the slot of the token's i-th smallest expert id, the
-// order the combine adds experts in. min_w > 0: the layer's skip_small_experts (skip_small; dropped picks id -1).
+// Top-k: one wavefront per token (wave_topk). crank[t, slot] = the rank of the slot's expert id among the token's
+// k ids (ascending): the order the combine adds experts in, and the pick's entry in the grouping's table.
+// min_w > 0: the layer's skip_small_experts (skip_small; dropped picks id -1).
 template <int EJ>
 __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, int T, int E, int k, int renorm,
                                               int32_t* __restrict__ ids, float* __restrict__ wts,
-                                              int32_t* __restrict__ corder, float min_w) {
+                                              int32_t* __restrict__ crank, float min_w) {
     __shared__ uint32_t scratch[4][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t = blockIdx.x * 4 + wv;
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(256) void k_topk(const float* __restrict__ logits, 
     if (lane < k) {
         ids[static_cast<int64_t>(t) * k + lane] = id;
         wts[static_cast<int64_t>(t) * k + lane] = w;
-        if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
+        if (crank) crank[static_cast<int64_t>(t) * k + lane] = id_rank;
     }
 }
 
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(64 * kRsWaves) void k_router_parts(const float* __r
 template <int EJ, int NSEG>
 __device__ __forceinline__ void topk_parts(const float* __restrict__ parts, int nseg, const float* __restrict__ bias,
                                            int T, int E, int rows, int k, int renorm, int32_t* __restrict__ ids,
-                                           float* __restrict__ wts, int32_t* __restrict__ corder,
+                                           float* __restrict__ wts, int32_t* __restrict__ crank,
                                            float* __restrict__ sg, float min_w) {
     __shared__ float lg[64 * EJ];
     __shared__ uint32_t scratch[64];
@@ -304,7 +305,7 @@ __device__ __forceinline__ void topk_parts(const float* __restrict__ parts, int 
         if (lane < k) {
             ids[static_cast<int64_t>(t) * k + lane] = id;
             wts[static_cast<int64_t>(t) * k + lane] = wsel;
-            if (corder) corder[static_cast<int64_t>(t) * k + id_rank] = lane;
+            if (crank) crank[static_cast<int64_t>(t) * k + lane] = id_rank;
         }
     }
 }
@@ -313,9 +314,9 @@ template <int EJ, int NSEG>
 __global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ parts, int nseg,
                                                      const float* __restrict__ bias, int T, int E, int rows, int k,
                                                      int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                     int32_t* __restrict__ corder, float* __restrict__ sg,
+                                                     int32_t* __restrict__ crank, float* __restrict__ sg,
                                                      float min_w) {
-    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg, min_w);
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, crank, sg, min_w);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -324,9 +325,11 @@ __global__ __launch_bounds__(1024) void k_topk_parts(const float* __restrict__ p
 // among its expert's pairs is the popcount of the bits before it, so the result is deterministic and stable
 // (pairs of one expert stay in token order). Outputs:
 //   offsets[E+1]    first sorted position of each expert's pairs; offsets[E] = the pairs grouped (T*k less
-//                   the picks skip_small dropped, whose pair_pos is -1)
+//                   the picks skip_small dropped, which have no position)
 //   active[0]       number of experts with at least one pair; active[1..] those experts, ascending
-//   sorted[P]       pair id (t*k + slot) at each sorted position;  pair_pos[P] the inverse
+//   sorted[P]       pair id (t*k + slot) at each sorted position
+//   picks[P]        the combine's table: entry t*k + crank[q] of pair q = (its position | kPosBf16 for an MFMA
+//                   expert, or 0xFFFFFFFF for a dropped pick; the bits of its weight wts[q])
 // One chunk: k_sort_small. Many chunks: k_sort_hist (per-chunk bitmaps, counts and ranks) -> k_sort_scan (chunk
 // bases, offsets, active experts, tile lists) -> k_sort_scatter.
 
@@ -362,7 +365,7 @@ __device__ __forceinline__ int chunk_rank(const uint32_t* bits, int e, int t) {
 
 // With tiles non-null (an MFMA plan), the sort's single-workgroup stage also writes the GEMMs' tile lists, for the
 // experts with more than gemv_max pairs (and the shared expert); `active` then lists only the others (the GEMV
-// experts), and pair_pos flags the pairs of MFMA experts with kPosBf16.
+// experts), and the table entries of MFMA experts' pairs carry kPosBf16.
 struct TileOut {
     int4* tiles;
     int4* tiles_down;
@@ -390,24 +393,35 @@ __global__ __launch_bounds__(1024) void k_sort_hist(const int32_t* __restrict__ 
     }
 }
 
-// flag_above: pairs of experts with more than this many pairs get kPosBf16 in pair_pos (the MFMA experts)
+// The combine's table (picks): each token's entries in ascending expert id, so k_combine reads them in one pass
+// with no dependent load (the pair's position and weight come together).
+struct PickOut {
+    const int32_t* crank;  // [T, k] from the top-k
+    const float* wts;      // [T, k]
+    uint2* picks;          // [T, k]
+    __device__ __forceinline__ void put(int64_t q, int k, uint32_t entry, int rank, float w) const {
+        picks[q - q % k + rank] = make_uint2(entry, __builtin_bit_cast(uint32_t, w));
+    }
+};
+
+// flag_above: pairs of experts with more than this many pairs get kPosBf16 in their table entries (MFMA experts)
 __global__ __launch_bounds__(256) void k_sort_scatter(const int32_t* __restrict__ ids, int T, int k, int E,
                                                       const int32_t* __restrict__ rank,
                                                       const int32_t* __restrict__ hist,
                                                       const int32_t* __restrict__ offsets, int flag_above,
-                                                      int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos) {
+                                                      int32_t* __restrict__ sorted, PickOut po) {
     const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (p >= static_cast<int64_t>(T) * k) return;
     const int e = ids[p];
-    if (e < 0 || e >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
-        pair_pos[p] = -1;
-        return;
+    uint32_t entry = 0xFFFFFFFFu;  // a pick skip_small dropped (id -1): no position, the combine leaves it out
+    if (e >= 0 && e < E) {
+        const int c = static_cast<int>(p / k) / kSortChunk;
+        const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
+        const bool bf16 = offsets[e + 1] - offsets[e] > flag_above;
+        sorted[pos] = static_cast<int32_t>(p);
+        entry = static_cast<uint32_t>(pos) | (bf16 ? kPosBf16 : 0u);
     }
-    const int c = static_cast<int>(p / k) / kSortChunk;
-    const int pos = hist[static_cast<int64_t>(c) * E + e] + rank[p];
-    const bool bf16 = offsets[e + 1] - offsets[e] > flag_above;
-    sorted[pos] = static_cast<int32_t>(p);
-    pair_pos[p] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (bf16 ? kPosBf16 : 0u));
+    po.put(p, k, entry, po.crank[p], po.wts[p]);
 }
 
 // One chunk (T <= kSortChunk), a workgroup of 1024 threads: one thread per expert builds the stable counting sort
@@ -524,7 +538,7 @@ __global__ __launch_bounds__(64) void k_fork_gate(uint32_t* sync, uint32_t spin_
 
 __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int T, int k, int E,
                                            int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                           int32_t* __restrict__ sorted, int32_t* __restrict__ pair_pos, TileOut to,
+                                           int32_t* __restrict__ sorted, PickOut po, TileOut to,
                                            uint32_t* fork_sync, int withhold) {
     __shared__ int32_t lds_ids[kSortChunk * WL_MAX_TOPK];
     __shared__ uint32_t bits[kSortWords * 64 * kMaxEJ];  // expert e: words kSortWords e .. + kSortWords - 1
@@ -532,6 +546,9 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
     __shared__ int wsum[kSortSmallThreads / 64];
     const int tid = threadIdx.x;
     const int P = T * k;
+    // the table's inputs for pair q = tid, loaded with the ids (the only pair of a thread when P <= blockDim.x)
+    const int my_rank = tid < P ? po.crank[tid] : 0;
+    const float my_w = tid < P ? po.wts[tid] : 0.0f;
     for (int q = tid; q < P; q += blockDim.x) lds_ids[q] = ids[q];
     for (int i = tid; i < kSortWords * E; i += blockDim.x) bits[i] = 0u;
     __syncthreads();
@@ -579,14 +596,17 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
         __syncthreads();  // lds_off for every thread
         for (int q = tid; q < P; q += blockDim.x) {
             const int ex = lds_ids[q];
-            if (ex < 0 || ex >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
-                pair_pos[q] = -1;
-                continue;
+            uint32_t entry = 0xFFFFFFFFu;  // a pick skip_small dropped (id -1): the combine leaves it out
+            if (ex >= 0 && ex < E) {
+                const uint32_t o = lds_off[ex];
+                const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
+                sorted[pos] = q;
+                entry = static_cast<uint32_t>(pos) | (o & kPosBf16);
             }
-            const uint32_t o = lds_off[ex];
-            const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
-            sorted[pos] = q;
-            pair_pos[q] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (o & kPosBf16));
+            if (q == tid)
+                po.put(q, k, entry, my_rank, my_w);
+            else
+                po.put(q, k, entry, po.crank[q], po.wts[q]);
         }
         if (fork_sync) publish_grouping(fork_sync, withhold);
         return;
@@ -604,14 +624,17 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
     if (tid == 0) active[0] = total;
     for (int q = tid; q < P; q += blockDim.x) {
         const int ex = lds_ids[q];
-        if (ex < 0 || ex >= E) {  // a pick skip_small dropped (id -1): no position, the combine leaves it out
-            pair_pos[q] = -1;
-            continue;
+        uint32_t entry = 0xFFFFFFFFu;  // a pick skip_small dropped (id -1): the combine leaves it out
+        if (ex >= 0 && ex < E) {
+            const uint32_t o = lds_off[ex];
+            const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
+            sorted[pos] = q;
+            entry = static_cast<uint32_t>(pos) | (o & kPosBf16);
         }
-        const uint32_t o = lds_off[ex];
-        const int pos = static_cast<int>(o & ~kPosBf16) + chunk_rank(bits, ex, q / k);
-        sorted[pos] = q;
-        pair_pos[q] = static_cast<int32_t>(static_cast<uint32_t>(pos) | (o & kPosBf16));
+        if (q == tid)
+            po.put(q, k, entry, my_rank, my_w);
+        else
+            po.put(q, k, entry, po.crank[q], po.wts[q]);
     }
     if (to.tiles) {
         tile_list(to.tiles, to.n_tiles, kTileTokens, e, E, big ? c : 0, off, T, to.with_shared, wsum);
@@ -623,10 +646,9 @@ __device__ __forceinline__ void sort_small(const int32_t* __restrict__ ids, int 
 __global__ __launch_bounds__(kSortSmallThreads) void k_sort_small(const int32_t* __restrict__ ids, int T, int k,
                                                                   int E, int32_t* __restrict__ offsets,
                                                                   int32_t* __restrict__ active,
-                                                                  int32_t* __restrict__ sorted,
-                                                                  int32_t* __restrict__ pair_pos, TileOut to,
-                                                                  uint32_t* fork_sync, int withhold) {
-    sort_small(ids, T, k, E, offsets, active, sorted, pair_pos, to, fork_sync, withhold);
+                                                                  int32_t* __restrict__ sorted, PickOut po,
+                                                                  TileOut to, uint32_t* fork_sync, int withhold) {
+    sort_small(ids, T, k, E, offsets, active, sorted, po, to, fork_sync, withhold);
 }
 
 static_assert(kRouterPartsMaxT <= kSortChunk, "k_topk_group groups its tokens as one chunk");
@@ -636,7 +658,7 @@ struct GroupOut {
     int32_t* offsets;
     int32_t* active;
     int32_t* sorted;
-    int32_t* pair_pos;
+    PickOut po;
     TileOut to;
     uint32_t* sync;  // kTopkDone; the fork-scope words when fork
     int fork;
@@ -651,10 +673,10 @@ template <int EJ, int NSEG>
 __global__ __launch_bounds__(1024) void k_topk_group(const float* __restrict__ parts, int nseg,
                                                      const float* __restrict__ bias, int T, int E, int rows, int k,
                                                      int renorm, int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                     int32_t* __restrict__ corder, float* __restrict__ sg,
+                                                     int32_t* __restrict__ crank, float* __restrict__ sg,
                                                      GroupOut g, float min_w) {
     __shared__ int last;
-    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, corder, sg, min_w);
+    topk_parts<EJ, NSEG>(parts, nseg, bias, T, E, rows, k, renorm, ids, wts, crank, sg, min_w);
     __syncthreads();  // the picks are stored by wavefront 0, whose thread 0 counts the workgroup done
     if (threadIdx.x == 0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -668,8 +690,7 @@ __global__ __launch_bounds__(1024) void k_topk_group(const float* __restrict__ p
     }
     __syncthreads();
     if (last)
-        sort_small(ids, T, k, E, g.offsets, g.active, g.sorted, g.pair_pos, g.to, g.fork ? g.sync : nullptr,
-                   g.withhold);
+        sort_small(ids, T, k, E, g.offsets, g.active, g.sorted, g.po, g.to, g.fork ? g.sync : nullptr, g.withhold);
 }
 
 // Many chunks: one thread per expert turns its per-chunk counts (hist[c][e]) into the chunk's first sorted
@@ -1131,12 +1152,12 @@ __global__ __launch_bounds__(256) void k_down(ExpertArgs a, int chunk) {
 }
 
 // y[t, r] = sum over the token's experts in ascending id of w * o[pos, r], then + sg[t] * o_sh[t, r]. A workgroup
-// takes kCombineSpan values of one token, 8 per thread, so the token's routing (indices and weights, the same for
-// the whole workgroup) is read with scalar loads once per workgroup. For k <= 8 every index and weight is loaded
-// first and then every o row, so the loads overlap instead of forming k dependent chains; the sum is the same in
-// both forms. Position pos's output row starts at byte 4 H pos of o: fp32 from a GEMV expert, or bf16 (its first
-// 2 H bytes) from an MFMA expert, which pair_pos marks with kPosBf16. SH: the shared expert's output type (float or
-// uint16_t for bf16, rows of H). H is a multiple of 8.
+// takes kCombineSpan values of one token, 8 per thread, so the token's table entries (picks: position and weight,
+// already in ascending expert id, the same for the whole workgroup) are read with scalar loads once per workgroup.
+// For k <= 8 every entry is loaded first and then every o row, so the loads overlap instead of forming k dependent
+// chains; the sum is the same in both forms. Position pos's output row starts at byte 4 H pos of o: fp32 from a
+// GEMV expert, or bf16 (its first 2 H bytes) from an MFMA expert, which its entry marks with kPosBf16. SH: the
+// shared expert's output type (float or uint16_t for bf16, rows of H). H is a multiple of 8.
 constexpr int kCombineUnroll = 8;
 constexpr int kCombineSpan = 8 * 256;
 
@@ -1160,9 +1181,8 @@ __device__ __forceinline__ Float8 load_o8(const float* o, int64_t pos, int H, in
 }
 
 template <typename SH>
-__global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int32_t* __restrict__ corder,
-                                                 const int32_t* __restrict__ pair_pos,
-                                                 const float* __restrict__ wts, const float* __restrict__ o,
+__global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const uint2* __restrict__ picks,
+                                                 const float* __restrict__ o,
                                                  const SH* __restrict__ o_sh, const float* __restrict__ sg,
                                                  const float* __restrict__ resid, float* __restrict__ y,
                                                  const uint32_t* status) {
@@ -1198,9 +1218,8 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             a1.w += wv * ov.b.w;
         }
     };
-    // a pair's position (-1 when out of range: never for ids from k_topk; guards caller-supplied ids) and flag
-    auto position = [&](int64_t q, bool& bf16) {
-        const uint32_t pp = static_cast<uint32_t>(pair_pos[q]);
+    // an entry's position (-1 for a dropped pick, whose entry is 0xFFFFFFFF, or out of range) and flag
+    auto position = [&](uint32_t pp, bool& bf16) {
         bf16 = (pp & kPosBf16) != 0;
         const int pos = static_cast<int>(pp & ~kPosBf16);
         return pos < P ? pos : -1;
@@ -1215,9 +1234,9 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             bf[n] = false;
             wv[n] = 0.0f;
             if (n < k) {
-                const int64_t q = base + corder[base + n];
-                pos[n] = position(q, bf[n]);
-                wv[n] = wts[q];
+                const uint2 e = picks[base + n];
+                pos[n] = position(e.x, bf[n]);
+                wv[n] = __builtin_bit_cast(float, e.y);
             }
         }
         Float8 ov[kCombineUnroll];
@@ -1229,11 +1248,11 @@ __global__ __launch_bounds__(256) void k_combine(int T, int H, int k, const int3
             if (n < k && pos[n] >= 0) add(n, wv[n], ov[n]);
     } else {
         for (int n = 0; n < k; n++) {
-            const int64_t q = base + corder[base + n];
+            const uint2 e = picks[base + n];
             bool bf16;
-            const int pos = position(q, bf16);
+            const int pos = position(e.x, bf16);
             if (pos < 0) continue;
-            add(n, wts[q], load_o8(o, pos, H, r, bf16));
+            add(n, __builtin_bit_cast(float, e.y), load_o8(o, pos, H, r, bf16));
         }
     }
     if (o_sh) {
@@ -1290,13 +1309,13 @@ Workspace carve(const WlMoeLayer& L, int64_t T, void* base) {
     w.sg = static_cast<float*>(take(sizeof(float) * T));
     w.ids = static_cast<int32_t*>(take(sizeof(int32_t) * P));
     w.wts = static_cast<float*>(take(sizeof(float) * P));
-    w.corder = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.crank = static_cast<int32_t*>(take(sizeof(int32_t) * P));
     w.rank = static_cast<int32_t*>(take(sizeof(int32_t) * P));
     w.hist = static_cast<int32_t*>(take(sizeof(int32_t) * nchunks * L.n_experts));
     w.offsets = static_cast<int32_t*>(take(sizeof(int32_t) * (L.n_experts + 1)));
     w.active = static_cast<int32_t*>(take(sizeof(int32_t) * (L.n_experts + 1)));
     w.sorted = static_cast<int32_t*>(take(sizeof(int32_t) * P));
-    w.pair_pos = static_cast<int32_t*>(take(sizeof(int32_t) * P));
+    w.picks = static_cast<uint2*>(take(sizeof(uint2) * P));
     w.h = static_cast<float*>(take(sizeof(float) * P * L.inter));
     w.o = static_cast<float*>(take(sizeof(float) * P * L.hidden));
     w.h_sh = static_cast<float*>(take(shared ? sizeof(float) * T * L.shared_inter : 0));
@@ -1373,19 +1392,19 @@ static int launch_router(const WlMoeLayer& L, const float* x, int64_t T, float* 
 }
 
 static int launch_topk(const WlMoeLayer& L, const float* logits, int64_t T, int32_t* ids, float* wts,
-                       int32_t* corder, float min_w, hipStream_t s) {
+                       int32_t* crank, float min_w, hipStream_t s) {
     const int grid = static_cast<int>((T + 3) / 4);
     const int E = L.n_experts, k = L.top_k, rn = L.norm_topk_prob ? 1 : 0, Ti = static_cast<int>(T);
     if (E <= 64)
-        k_topk<1><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
+        k_topk<1><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, crank, min_w);
     else if (E <= 128)
-        k_topk<2><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
+        k_topk<2><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, crank, min_w);
     else if (E <= 256)
-        k_topk<4><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
+        k_topk<4><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, crank, min_w);
     else if (E <= 512)
-        k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
+        k_topk<8><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, crank, min_w);
     else
-        k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, corder, min_w);
+        k_topk<16><<<grid, 256, 0, s>>>(logits, Ti, E, k, rn, ids, wts, crank, min_w);
     return launch_status();
 }
 
@@ -1420,7 +1439,7 @@ static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w,
         };
         auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
         kernel<<<grid, kSortSmallThreads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts,
-                                                  w.corder, sg, *g, L.min_expert_weight);
+                                                  w.crank, sg, *g, L.min_expert_weight);
         return launch_status();
     }
     auto pick = [&](auto seg32) {
@@ -1429,7 +1448,7 @@ static int launch_topk_parts(const WlMoeLayer& L, int64_t T, const Workspace& w,
                : E <= 512 ? k_topk_parts<8, S> : k_topk_parts<16, S>;
     };
     auto kernel = nseg == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
-    kernel<<<grid, threads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts, w.corder, sg,
+    kernel<<<grid, threads, 0, s>>>(w.parts, nseg, L.router_bias, Ti, E, rows, k, rn, w.ids, w.wts, w.crank, sg,
                                     L.min_expert_weight);
     return launch_status();
 }
@@ -1443,7 +1462,8 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
     const int nchunks = static_cast<int>((T + kSortChunk - 1) / kSortChunk);
     if (nchunks == 1) {
         k_sort_small<<<1, kSortSmallThreads, 0, s>>>(ids, static_cast<int>(T), k, E, w.offsets, w.active, w.sorted,
-                                                     w.pair_pos, to, fork ? w.sync : nullptr, withhold ? 1 : 0);
+                                                     PickOut{w.crank, w.wts, w.picks}, to, fork ? w.sync : nullptr,
+                                                     withhold ? 1 : 0);
     } else {
         const size_t lds = sizeof(uint32_t) * E * kSortWords + sizeof(int32_t) * E;
         k_sort_hist<<<nchunks, 1024, lds, s>>>(ids, static_cast<int>(T), k, E, w.rank, w.hist);
@@ -1452,7 +1472,7 @@ static int launch_sort(const WlMoeLayer& L, const Workspace& w, const int32_t* i
         const int64_t P = T * k;
         k_sort_scatter<<<static_cast<int>((P + 255) / 256), 256, 0, s>>>(
             ids, static_cast<int>(T), k, E, w.rank, w.hist, w.offsets, tiles ? gemv_max : 0x7FFFFFFF, w.sorted,
-            w.pair_pos);
+            PickOut{w.crank, w.wts, w.picks});
         if (fork)
             k_fork_store<<<1, 64, 0, s>>>(w.sync + kForkDone, 0u, withhold ? nullptr : w.sync + kForkSorted, 1u);
     }
@@ -1758,7 +1778,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
         if (rc) return rc;
         mark(1);
         // the grouping in the same launch (mark 3 follows mark 2 at once)
-        const GroupOut g{w.offsets, w.active, w.sorted, w.pair_pos,
+        const GroupOut g{w.offsets, w.active, w.sorted, PickOut{w.crank, w.wts, w.picks},
                          TileOut{mfma ? w.tiles : nullptr, w.tiles_down, w.n_tiles, L.shared_gate_up ? 1 : 0, gemv_max},
                          w.sync, in_scope ? 1 : 0, starve ? 1 : 0};
         rc = launch_topk_parts(L, tokens, w, sg, &g, s);
@@ -1770,7 +1790,7 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
                  : launch_router(L, x, tokens, w.logits, sg, mfma ? w.xb : nullptr, s);
         if (rc) return rc;
         mark(1);
-        rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.corder, L.min_expert_weight, s);
+        rc = launch_topk(L, w.logits, tokens, w.ids, w.wts, w.crank, L.min_expert_weight, s);
         if (rc) return rc;
         mark(2);
     }
@@ -1832,13 +1852,12 @@ static int run_layer(const WlMoeLayer* layer, const float* x, int64_t tokens, fl
     mark(5);
     const unsigned cgrid = static_cast<unsigned>(tokens * ((L.hidden + kCombineSpan - 1) / kCombineSpan));
     if (mfma)
-        k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                                  w.wts, w.o,
+        k_combine<uint16_t><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.picks, w.o,
                                                   shared ? reinterpret_cast<const uint16_t*>(w.o_sh) : nullptr, sg,
                                                   resid, y, combine_status);
     else
-        k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.corder, w.pair_pos,
-                                               w.wts, w.o, shared ? w.o_sh : nullptr, sg, resid, y, combine_status);
+        k_combine<float><<<cgrid, 256, 0, s>>>(static_cast<int>(tokens), L.hidden, L.top_k, w.picks, w.o,
+                                               shared ? w.o_sh : nullptr, sg, resid, y, combine_status);
     rc = launch_status();
     mark(6);
     return rc;
