@@ -698,32 +698,50 @@ def run_prefill(torch, hip, layers, T, steps):
 
 
 def run_linear(torch, hip, rows=2048, k=2048, T=4096, reps=20):
-    """A quantized non-expert weight in a 4096-token prefill: GGMLWeight's F.linear above 8 tokens, as wl_linear
-    (bf16 MFMA, weights dequantized in registers) and as the reference's form (dequantize_gpu to bf16, then a bf16
-    matmul; gguf/metal.py:407), timed with events over `reps` calls each."""
+    """A quantized non-expert weight in a 4096-token prefill: GGMLWeight's F.linear above 8 tokens (its bf16 values
+    dequantized once and kept, then the library's bf16 GEMM), wl_linear (bf16 MFMA with the weights dequantized in
+    registers, nothing kept) and the reference's form (dequantize_gpu to bf16 on every call, then a bf16 matmul;
+    gguf/metal.py:407), each as `reps` calls in one graph replay."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
     raw = gen_q4k(torch, rows * (k // 256), gen).view(-1)
     x = torch.randn(T, k, device="cuda", generator=gen).to(torch.bfloat16)
 
     def timed(fn):
+        # `reps` calls captured in one graph and replayed, so the figure is GPU time, not Python dispatch (the
+        # first call, outside the capture, also builds GGMLWeight's kept bf16 values)
         fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        for _ in range(reps):
-            fn()
+        g.replay()
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) * 1000.0 / reps
 
+    weight = hip.GGMLWeight(raw, "Q4_K", (rows, k))
+    us_kept = timed(lambda: torch.nn.functional.linear(x, weight))
     us_mfma = timed(lambda: hip.linear_mfma(raw, "Q4_K", (rows, k), x))
     us_ref = timed(lambda: torch.nn.functional.linear(x, hip.dequantize_gpu(raw, "Q4_K", (rows, k))))
+    # the vendor library's bf16 GEMM alone on the same shape (the weight dequantized beforehand, outside the timing):
+    # what this problem size allows a tuned dense GEMM
+    wb = hip.dequantize_gpu(raw, "Q4_K", (rows, k))
+    us_gemm = timed(lambda: torch.nn.functional.linear(x, wb))
     flops = 2.0 * T * rows * k
-    log(f"linear Q4_K {rows}x{k}, {T} tokens: wl_linear {us_mfma:.1f} us ({flops / us_mfma / 1e6:.0f} TFLOP/s), "
-        f"dequantize + bf16 matmul {us_ref:.1f} us")
-    return {"rows": rows, "k": k, "tokens": T, "us_wl_linear": round(us_mfma, 2),
-            "us_dequantize_matmul": round(us_ref, 2), "tflops_wl_linear": round(flops / us_mfma / 1e6, 1)}
+    log(f"linear Q4_K {rows}x{k}, {T} tokens: GGMLWeight F.linear (bf16 kept) {us_kept:.1f} us "
+        f"({flops / us_kept / 1e6:.0f} TFLOP/s), wl_linear {us_mfma:.1f} us ({flops / us_mfma / 1e6:.0f} TFLOP/s), "
+        f"dequantize + bf16 matmul per call {us_ref:.1f} us, the bf16 matmul alone {us_gemm:.1f} us "
+        f"({flops / us_gemm / 1e6:.0f} TFLOP/s)")
+    return {"rows": rows, "k": k, "tokens": T, "us_ggml_linear_kept": round(us_kept, 2),
+            "tflops_ggml_linear_kept": round(flops / us_kept / 1e6, 1), "us_wl_linear": round(us_mfma, 2),
+            "us_dequantize_matmul": round(us_ref, 2), "tflops_wl_linear": round(flops / us_mfma / 1e6, 1),
+            "us_bf16_matmul_alone": round(us_gemm, 2), "tflops_bf16_matmul_alone": round(flops / us_gemm / 1e6, 1)}
 
 
 def run_gguf_load(torch, n_layers):

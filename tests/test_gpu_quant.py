@@ -107,6 +107,28 @@ def test_ggml_weight_linear(hip):
     assert offset == 0 and base.numel() == w.size
 
 
+def test_ggml_weight_linear_routes(hip):
+    """Above MAX_TOKENS: with keep_dense (the default) the bf16 values are dequantized once and kept, and each call is
+    the reference's bf16 F.linear on them (gguf/metal.py:407), bit for bit; with keep_dense False wl_linear runs
+    (weights dequantized in registers, nothing kept), within the bf16 output rounding."""
+    rng = np.random.default_rng(14)
+    w = synth.matrix(rng, "Q6_K", 512, 2048)
+    weight = hip.GGMLWeight(dev(w).reshape(-1), "Q6_K", (512, 2048))
+    x = torch.randn(70, 2048, generator=torch.Generator().manual_seed(15)).cuda()
+    want = F.linear(x.to(torch.bfloat16), hip.dequantize_gpu(weight.raw, "Q6_K", (512, 2048))).float()
+    y = F.linear(x, weight)
+    kept = weight.dense()
+    assert torch.equal(y, want)
+    assert torch.equal(F.linear(x, weight), want) and weight.dense() is kept  # dequantized once
+    dense = torch.from_numpy(q.dequantize_matrix(w, "Q6_K", 512, 2048))
+    assert torch.equal(kept.float().cpu(), dense.to(torch.bfloat16).float())  # the blocks' values, rounded to bf16
+    weight.drop_dense()
+    weight.keep_dense = False
+    y2 = F.linear(x, weight)
+    assert weight._dense is None
+    assert moe_ref.rel_err(y2.cpu().numpy(), want.cpu().numpy()) < 4e-3
+
+
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("rows,k", [(256, 256), (512, 2048), (2048, 512)])
 @pytest.mark.parametrize("tokens", [9, 20, 64, 65, 130, 300])

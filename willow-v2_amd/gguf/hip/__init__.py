@@ -243,7 +243,15 @@ def dequantize_gpu(raw: torch.Tensor, type_name: str, shape: tuple, dtype: torch
 class GGMLWeight:
     """A [rows, k] weight kept as its ggml blocks on the GPU, used in place of a dense tensor: F.linear(x, weight)
     runs the HIP kernels (through __torch_function__), as gguf/metal.py:365-408. raw is a uint8 tensor on the GPU
-    (a view into the HBM-resident expert store) or on the CPU, in which case it is copied over on first use."""
+    (a view into the HBM-resident expert store) or on the CPU, in which case it is copied over on first use.
+
+    Above MAX_TOKENS tokens the reference dequantizes the weight to bf16 on every call and runs a bf16 F.linear
+    (gguf/metal.py:407). With keep_dense (the default) the bf16 values are dequantized once, on the first such call,
+    and kept in HBM beside the blocks (2 bytes per value; the non-expert weights are a few GB at most against 288 GB),
+    so each call is the same bf16 F.linear on the same values, the library GEMM alone. With keep_dense False nothing
+    is kept: wl_linear runs the product with the weights dequantized in registers (no bf16 copy, slower)."""
+
+    keep_dense = True
 
     @classmethod
     def __torch_function__(cls, func, types, args=(), kwargs=None):
@@ -259,6 +267,7 @@ class GGMLWeight:
             raise ValueError(f"{raw.numel()} bytes do not hold a {type_name} {self.shape} matrix")
         self.nbytes = raw.numel()
         self.device = raw.device if raw.is_cuda else torch.device("cuda")
+        self._dense = None
 
     def to_gpu(self):
         if not self.raw.is_cuda:
@@ -271,11 +280,25 @@ class GGMLWeight:
         base = self.raw if self.raw._base is None else self.raw._base
         return base, self.raw.storage_offset() - base.storage_offset()
 
+    def dense(self) -> torch.Tensor:
+        """The weight's values as bf16 [rows, k] on the GPU: dequantized once (bit-exact with gguf/quants.py, rounded
+        to bf16 as gguf/metal.py:357-363 does), then kept until drop_dense()."""
+        if self._dense is None:
+            self.to_gpu()
+            self._dense = dequantize_gpu(self.raw, self.type_name, self.shape)
+        return self._dense
+
+    def drop_dense(self):
+        """Frees the kept bf16 values (the next call above MAX_TOKENS with keep_dense dequantizes again)."""
+        self._dense = None
+
     def linear(self, x: torch.Tensor) -> torch.Tensor:
         self.to_gpu()
         flat = x.reshape(-1, x.shape[-1]).to(self.device)
         if flat.shape[0] <= MAX_TOKENS:
             y = gemv(self.raw, self.type_name, self.shape, flat).to(x.dtype)
+        elif self.keep_dense:  # the reference's arithmetic (gguf/metal.py:407) on bf16 values kept in HBM
+            y = F.linear(flat.to(torch.bfloat16), self.dense()).to(x.dtype)
         elif self.shape[0] % 256 == 0 and self.shape[1] % 256 == 0:
             y = linear_mfma(self.raw, self.type_name, self.shape, flat).to(x.dtype)
         else:  # the reference's own form (gguf/metal.py:407)
