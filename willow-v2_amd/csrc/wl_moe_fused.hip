@@ -112,11 +112,12 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset) into *dst(i) once
-// every one carries `tag` (workgroup-cooperative); false if kSpinLimit polls pass first. n <= 32 * blockDim.x.
-template <typename Src, typename Dst>
+// Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset), handing each to
+// put(i, value) once every one carries `tag` (workgroup-cooperative); false if kSpinLimit polls pass first.
+// n <= 32 * blockDim.x.
+template <typename Src, typename Put>
 __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit, Src src,
-                                              Dst dst) {
+                                              Put put) {
     uint32_t pending = 0;
     for (int q = 0; q < 32 && static_cast<int>(threadIdx.x) + q * static_cast<int>(blockDim.x) < n; q++)
         pending |= 1u << q;
@@ -129,7 +130,7 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
             const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(i)),
                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (static_cast<uint32_t>(w >> 32) == tag) {
-                *dst(i) = __builtin_bit_cast(float, static_cast<uint32_t>(w));
+                put(i, __builtin_bit_cast(float, static_cast<uint32_t>(w)));
                 pending &= ~(1u << q);
             }
         }
@@ -187,6 +188,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
+    __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
     __shared__ __attribute__((aligned(16))) float lds_xn[NORM ? kFusedMaxHidden : 4];  // NORM: the normalized x
@@ -362,12 +364,21 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     }
 
     // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
-    // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading.
+    // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading. As
+    // each expert logit lands, its order key (NaN as -inf) goes into its 32-logit group's maximum, which the top-k
+    // below needs: the maxima are formed while the gather waits, not after it.
+    if (threadIdx.x < kFusedMaxE / 32) lds_gmax[threadIdx.x] = 0u;
     __syncthreads();
-    ok = gather_tagged(
-             a.sync, n_logits + (shared ? I : 0), tag, a.spin_limit,
-             [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
-             [&](int i) { return i < n_logits ? &lds_logits[i] : &lds_hsh[i - n_logits]; }) &&
+    ok = gather_tagged(a.sync, n_logits + (shared ? I : 0), tag, a.spin_limit,
+                       [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
+                       [&](int i, float v) {
+                           if (i < n_logits) {
+                               lds_logits[i] = v;
+                               if (i < E) atomicMax(&lds_gmax[i >> 5], order_key(v == v ? v : -INFINITY));
+                           } else {
+                               lds_hsh[i - n_logits] = v;
+                           }
+                       }) &&
          ok;
     // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
     // slot u mod (8 G), so on workgroup u mod G: rows j = b, b + G, ... and their up rows), one 4-byte load per
@@ -387,8 +398,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         }
     }
-    // top-k, in wavefront 0. Lane l holds logits l + 64 j. The 8 groups of 32 logits (j, half of the wavefront)
-    // reduce their order keys to the maximum (DPP within rows of 16, then a row broadcast); with T0 the smallest
+    // top-k, in wavefront 0. Lane l holds logits l + 64 j. The groups of 32 logits (i / 32) have their largest order
+    // key in lds_gmax (formed during the gather); with T0 the smallest
     // maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at least k the
     // top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The candidates
     // (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are compacted
@@ -412,18 +423,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         const int ng = (E + 31) / 32;
         uint32_t t0 = 0xFFFFFFFFu;
 #pragma unroll
-        for (int j = 0; j < EJ; j++) {
-            int u = static_cast<int>(k32[j]);
-            u = umax_dpp<0xB1>(u);   // quad_perm [1,0,3,2]
-            u = umax_dpp<0x4E>(u);   // quad_perm [2,3,0,1]
-            u = umax_dpp<0x141>(u);  // row_half_mirror
-            u = umax_dpp<0x140>(u);  // row_mirror: every lane holds its row's maximum
-            // row_bcast:15 into rows 1 and 3: lanes 31 and 63 then hold the maxima of lanes 0..31 and 32..63
-            u = static_cast<int>(max(static_cast<uint32_t>(u),
-                                     static_cast<uint32_t>(__builtin_amdgcn_update_dpp(u, u, 0x142, 0xA, 0xF, false))));
-            if (2 * j < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 31)));
-            if (2 * j + 1 < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(u, 63)));
-        }
+        for (int g = 0; g < 2 * EJ; g++)  // the same word for every lane (a broadcast read)
+            if (g < ng) t0 = min(t0, lds_gmax[g]);
         if (ng < k) t0 = 0;
         lane_sync();
         int n_cand = 0;
@@ -447,13 +448,16 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             above[q] = 0;
         }
         if (n_cand <= 32) {
+            int above1 = 0;  // two counts, so the compares do not form one dependent chain
 #pragma unroll
             for (int u = 0; u < 32; u += 2) {
                 const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u]);
                 const uint64_t o0 = (static_cast<uint64_t>(r.y) << 32) | r.x;
                 const uint64_t o1 = (static_cast<uint64_t>(r.w) << 32) | r.z;
-                above[0] += (o0 > ck[0] ? 1 : 0) + (o1 > ck[0] ? 1 : 0);
+                above[0] += o0 > ck[0] ? 1 : 0;
+                above1 += o1 > ck[0] ? 1 : 0;
             }
+            above[0] += above1;
         } else {
             for (int u0 = 0; u0 < n_cand; u0 += 2) {  // entries past n_cand (< kFusedMaxE) are never counted
                 const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u0]);
