@@ -99,6 +99,12 @@ __device__ __forceinline__ float router_row_xw(XF x4, WF w4, bool valid, int H, 
     return total;
 }
 
+// the number of lanes below this one whose bit is set in the wavefront mask m (v_mbcnt_lo / v_mbcnt_hi)
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
 // float -> uint32 with the same order (larger float, larger key)
 __device__ __forceinline__ uint32_t order_key(float v) {
     const uint32_t u = __builtin_bit_cast(uint32_t, v);

@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const bool cand = valid[j] && k32[j] >= t0;
             const uint64_t m = __ballot(cand);
             if (cand)
-                lds_cand[n_cand + __popcll(m & __lanemask_lt())] =
+                lds_cand[n_cand + lanes_below(m)] =
                     (static_cast<uint64_t>(k32[j]) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(idx));
             n_cand += __popcll(m);
         }
@@ -474,8 +474,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                 lds_pick[above[q]] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck[q]));
         lane_sync();
         // the picks in ascending id order for the tasks; the weights (needed only by the final sum) come later
-        const int my_id = lane < k ? lds_pick[lane] : 0;
         if (a.min_w > 0.0f) {
+            const int my_id = lane < k ? lds_pick[lane] : 0;
             // skip_small_experts: which picks run depends on the weights, so they are computed here, before any
             // gate_up load (the same arithmetic as below); only the kept picks become tasks
             const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
@@ -501,13 +501,17 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
             if (lane == 0) lds_kk = __popcll(kept);
         } else {
-            int idr[kFusedMaxK];
+            // the candidates were compacted in ascending id order, so a pick's place among the k ids is the number
+            // of picks before it in the list
+            int before = 0;
 #pragma unroll
-            for (int q = 0; q < kFusedMaxK; q++) idr[q] = __builtin_amdgcn_readlane(my_id, q);
-            int my_rank = 0;  // position among the k ids in ascending order
-#pragma unroll
-            for (int q = 0; q < kFusedMaxK; q++) my_rank += (q < k && idr[q] < my_id) ? 1 : 0;
-            if (lane < k) lds_sel[my_rank] = my_id;
+            for (int q = 0; q < EJ; q++) {
+                const bool picked = lane + 64 * q < n_cand && above[q] < k;
+                const uint64_t pm = __ballot(picked);
+                if (picked)
+                    lds_sel[before + lanes_below(pm)] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck[q]));
+                before += __popcll(pm);
+            }
             if (lane == 0) lds_kk = k;
         }
     }
