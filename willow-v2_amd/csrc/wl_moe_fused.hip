@@ -191,7 +191,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
-    __shared__ __attribute__((aligned(16))) float lds_xn[NORM ? kFusedMaxHidden : 4];  // NORM: the normalized x
+    __shared__ __attribute__((aligned(16))) float lds_xn[kFusedMaxHidden];  // x (NORM: normalized), for every read
     // GUESS (the next-layer guess): x normalized with the next layer's RMSNorm; the previous call's guess (ids)
     __shared__ __attribute__((aligned(16))) float lds_xg[GUESS ? kFusedMaxHidden : 4];
     __shared__ int lds_gsel[GUESS ? kFusedMaxK : 1];
@@ -217,16 +217,18 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     const bool publish = b != a.silent_wg;
 
     // The layer's input: x, or with NORM its RMSNorm, written once to LDS by the workgroup. Thread i loads x's
-    // values 4i..4i+3 (and the norm weight's), so x crosses from L2 once per workgroup; wavefront 0 takes the sum of
-    // squares from LDS in the router's order (router_row of x with itself); then every thread normalizes its four
-    // values in place. Every wavefront reading all of x from global memory for its own sum of squares instead
-    // takes ~8 us at this grid (2048 wavefronts on the same 64 lines).
+    // values 4i..4i+3 (and the norm weight's), so x crosses from L2 once per workgroup, in coalesced loads; with
+    // NORM wavefront 0 then takes the sum of squares from LDS in the router's order (router_row of x with itself)
+    // and every thread normalizes its four values in place. Every later read of x (router rows, gate_up runs) comes
+    // from LDS: a router lane's own 64-value segment read from global memory takes 16 loads that each touch 32
+    // lines, in every wavefront. (Every wavefront reading all of x from global memory for its own sum of squares
+    // took ~8 us at this grid: 2048 wavefronts on the same 64 lines.)
     static_assert(kFusedMaxHidden / 4 <= kFusedThreads, "one float4 of x per thread");
     static_assert(kFusedMaxHidden <= 32 * kRouterSeg, "a router row: one 64-value segment per lane of a half-wave");
-    // With NORM, a wavefront whose first phase-A task is a router row requests that row (lane s < 32: segment s)
-    // before the norm prologue, so its latency overlaps the wait for x instead of following the prologue.
+    // A wavefront whose first phase-A task is a router row requests that row (lane s < 32: segment s) before the
+    // prologue, so its latency overlaps the wait for x instead of following the prologue.
     float4 wpre[kRouterSeg / 4];
-    if constexpr (NORM) {
+    {
         if (slot < n_logits && lane < H / kRouterSeg) {
             const float* wr0 = slot < E ? a.router + static_cast<int64_t>(slot) * H : a.sh_gate;
 #pragma unroll
@@ -261,13 +263,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                                                                             lds_inv_g);
         }
         __syncthreads();
+    } else {
+        if (static_cast<int>(threadIdx.x) < H / 4)
+            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
+        __syncthreads();
     }
-    auto xload = [&](int i) -> float4 {
-        if constexpr (NORM)
-            return reinterpret_cast<const float4*>(lds_xn)[i];
-        else
-            return reinterpret_cast<const float4*>(a.x)[i];
-    };
+    auto xload = [&](int i) -> float4 { return reinterpret_cast<const float4*>(lds_xn)[i]; };
 
     // x, for the gate_up dot products: a lane's two 16-value runs of its block gi
     const int nb = H / kQK;  // <= 8: one gate/up block per lane group
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const bool valid = lane < 32;
             const float* wr = row < E ? a.router + static_cast<int64_t>(row) * H : a.sh_gate;
             float total;
-            if (NORM && t == slot)  // the row requested before the norm prologue
+            if (t == slot)  // the row requested before the prologue
                 total = router_row_xw(xload, [&](int, int i) { return wpre[i]; }, valid, H, lane);
             else
                 total = router_row_x(xload, wr, valid, H, lane);
