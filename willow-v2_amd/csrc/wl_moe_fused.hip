@@ -191,7 +191,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
-    __shared__ __attribute__((aligned(16))) float lds_xn[kFusedMaxHidden];  // x (NORM: normalized), for every read
+    // x (NORM: normalized) for every read, 4 floats of padding after every 64 values (x_slot)
+    __shared__ __attribute__((aligned(16))) float lds_xn[kFusedMaxHidden + kFusedMaxHidden / 16];
     // GUESS (the next-layer guess): x normalized with the next layer's RMSNorm; the previous call's guess (ids)
     __shared__ __attribute__((aligned(16))) float lds_xg[GUESS ? kFusedMaxHidden : 4];
     __shared__ int lds_gsel[GUESS ? kFusedMaxK : 1];
@@ -237,6 +238,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
     }
     const bool guess = GUESS && a.guess_router != nullptr;
+    // float4 i of x sits at float4 x_slot(i) of lds_xn: a router lane's 64-value segment then starts 4 banks past
+    // its neighbour's instead of on the same ones (a 4-way instead of a 32-way conflict)
+    auto x_slot = [](int i) { return i + (i >> 4); };
+    auto xload = [&](int i) -> float4 { return reinterpret_cast<const float4*>(lds_xn)[x_slot(i)]; };
     if constexpr (NORM) {
         __shared__ float lds_inv, lds_inv_g;
         const bool mine = static_cast<int>(threadIdx.x) < H / 4;
@@ -245,11 +250,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             xv = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
             if (a.norm_w) nw = reinterpret_cast<const float4*>(a.norm_w)[threadIdx.x];
             if (guess && a.guess_norm_w) gw = reinterpret_cast<const float4*>(a.guess_norm_w)[threadIdx.x];
-            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = xv;
+            reinterpret_cast<float4*>(lds_xn)[x_slot(threadIdx.x)] = xv;
         }
         __syncthreads();
         if (wv == 0) {
-            const float ss = router_row(lds_xn, lds_xn, true, H, lane);
+            const float ss = router_row_xw(xload, [&](int sg, int i) { return xload(sg * (kRouterSeg / 4) + i); },
+                                           true, H, lane);
             if (lane == 0) {
                 lds_inv = norm_inv(ss, H, a.norm_eps);
                 lds_inv_g = norm_inv(ss, H, a.guess_eps);  // the same x: only the weight and eps differ
@@ -257,7 +263,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
         __syncthreads();
         if (mine) {
-            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = norm_apply(xv, a.norm_w != nullptr, nw, lds_inv);
+            reinterpret_cast<float4*>(lds_xn)[x_slot(threadIdx.x)] =
+                norm_apply(xv, a.norm_w != nullptr, nw, lds_inv);
             if (guess)
                 reinterpret_cast<float4*>(lds_xg)[threadIdx.x] = norm_apply(xv, a.guess_norm_w != nullptr, gw,
                                                                             lds_inv_g);
@@ -265,10 +272,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         __syncthreads();
     } else {
         if (static_cast<int>(threadIdx.x) < H / 4)
-            reinterpret_cast<float4*>(lds_xn)[threadIdx.x] = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
+            reinterpret_cast<float4*>(lds_xn)[x_slot(threadIdx.x)] =
+                reinterpret_cast<const float4*>(a.x)[threadIdx.x];
         __syncthreads();
     }
-    auto xload = [&](int i) -> float4 { return reinterpret_cast<const float4*>(lds_xn)[i]; };
+
 
     // x, for the gate_up dot products: a lane's two 16-value runs of its block gi
     const int nb = H / kQK;  // <= 8: one gate/up block per lane group
