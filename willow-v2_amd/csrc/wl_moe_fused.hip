@@ -113,31 +113,55 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
 }
 
 // Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset), handing each to
-// put(i, value) once every one carries `tag` (workgroup-cooperative); false if kSpinLimit polls pass first.
-// n <= 32 * blockDim.x.
-template <typename Src, typename Put>
+// put(i, value) once it carries `tag` (workgroup-cooperative: thread t polls values t + q blockDim.x, q < Q;
+// n <= Q blockDim.x); false if spin_limit polls pass first. Two polling rounds are in flight: a round's loads are
+// issued before the previous round's are checked, so a value is seen about half a load's round trip after it
+// lands instead of a whole one (the logits exchange of the b=1 decode: 15.88 -> 15.62 us per layer; three or four
+// rounds in flight measured slower, their extra loads queueing at the few lines every workgroup polls). Every
+// slot is loaded in every round (a value already in, or an index past n, reloads a word whose result is dropped),
+// so a round's loads are unconditional and the compiler keeps the older round outstanding while it checks.
+template <int Q, typename Src, typename Put>
 __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit, Src src,
                                               Put put) {
-    uint32_t pending = 0;
-    for (int q = 0; q < 32 && static_cast<int>(threadIdx.x) + q * static_cast<int>(blockDim.x) < n; q++)
-        pending |= 1u << q;
-    for (uint32_t spins = 0;; spins++) {
-        uint32_t m = pending;
-        while (m) {
-            const int q = __builtin_ctz(m);
-            m &= m - 1;
-            const int i = threadIdx.x + q * blockDim.x;
-            const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(sync + src(i)),
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (static_cast<uint32_t>(w >> 32) == tag) {
-                put(i, __builtin_bit_cast(float, static_cast<uint32_t>(w)));
-                pending &= ~(1u << q);
-            }
-        }
-        if (__syncthreads_and(pending == 0)) return true;
-        if (spins >= spin_limit) return false;
-        __builtin_amdgcn_s_sleep(1);
+    const uint64_t* w[Q];
+    bool pend[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int i = threadIdx.x + q * blockDim.x;
+        pend[q] = i < n;
+        w[q] = reinterpret_cast<const uint64_t*>(sync + src(pend[q] ? i : 0));
     }
+    auto ld = [](const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto waiting = [&] {
+        bool r = false;
+#pragma unroll
+        for (int q = 0; q < Q; q++) r = r || pend[q];
+        return r;
+    };
+    auto check = [&](const uint64_t (&v)[Q]) {
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (pend[q] && static_cast<uint32_t>(v[q] >> 32) == tag) {
+                put(threadIdx.x + q * blockDim.x, __builtin_bit_cast(float, static_cast<uint32_t>(v[q])));
+                pend[q] = false;
+            }
+    };
+    uint64_t ra[Q], rb[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) ra[q] = ld(w[q]);
+    for (uint32_t spins = 0; spins <= spin_limit; spins += 2) {
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 0; q < Q; q++) rb[q] = ld(w[q]);
+        check(ra);
+        if (!waiting()) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 0; q < Q; q++) ra[q] = ld(w[q]);
+        check(rb);
+        if (!waiting()) break;
+    }
+    return __syncthreads_and(!waiting());
 }
 
 // The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. It first waits on the last
@@ -188,6 +212,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
+    __shared__ uint32_t lds_key[kFusedMaxE];        // the expert logits' order keys (NaN as -inf)
     __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
@@ -374,21 +399,30 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
 
     // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
     // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading. As
-    // each expert logit lands, its order key (NaN as -inf) goes into its 32-logit group's maximum, which the top-k
-    // below needs: the maxima are formed while the gather waits, not after it.
+    // each expert logit lands, its order key (NaN as -inf) goes to lds_key and into its 32-logit group's maximum,
+    // which the top-k below needs: the keys and maxima are formed while the gather waits, not after it.
     if (threadIdx.x < kFusedMaxE / 32) lds_gmax[threadIdx.x] = 0u;
     __syncthreads();
-    ok = gather_tagged(a.sync, n_logits + (shared ? I : 0), tag, a.spin_limit,
-                       [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); },
-                       [&](int i, float v) {
-                           if (i < n_logits) {
-                               lds_logits[i] = v;
-                               if (i < E) atomicMax(&lds_gmax[i >> 5], order_key(v == v ? v : -INFINITY));
-                           } else {
-                               lds_hsh[i - n_logits] = v;
-                           }
-                       }) &&
-         ok;
+    {
+        const int n_route = n_logits + (shared ? I : 0);
+        auto src = [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); };
+        auto put = [&](int i, float v) {
+            if (i < n_logits) {
+                lds_logits[i] = v;
+                if (i < E) {
+                    const uint32_t kv = order_key(v == v ? v : -INFINITY);
+                    lds_key[i] = kv;
+                    atomicMax(&lds_gmax[i >> 5], kv);
+                }
+            } else {
+                lds_hsh[i - n_logits] = v;
+            }
+        };
+        static_assert(3 * kFusedThreads >= kFusedMaxE + 1 + kFusedMaxInter, "three values per thread at most");
+        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put)
+                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put)) &&
+             ok;
+    }
     // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
     // slot u mod (8 G), so on workgroup u mod G: rows j = b, b + G, ... and their up rows), one 4-byte load per
     // 128-byte line, spread over wavefronts 1 .. 7 while wavefront 0 runs the top-k: HBM carries nothing else then,
@@ -407,26 +441,23 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         }
     }
-    // top-k, in wavefront 0. Lane l holds logits l + 64 j. The groups of 32 logits (i / 32) have their largest order
-    // key in lds_gmax (formed during the gather); with T0 the smallest
-    // maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at least k the
-    // top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The candidates
-    // (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are compacted
-    // in LDS and each counts the candidates above it: up to 32 of them in one fixed pass over a zero-padded list.
-    // The k of rank < k place themselves; their weights (wave_topk's arithmetic) are computed after the gate_up
-    // loads have been issued.
+    // top-k, in wavefront 0. Lane l holds the order keys of logits l + 64 j (lds_key, written by the gather). The
+    // groups of 32 logits (i / 32) have their largest order key in lds_gmax (formed during the gather); with T0 the
+    // smallest maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at
+    // least k the top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The
+    // candidates (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are
+    // compacted in LDS and each counts the candidates above it: up to 32 of them in one fixed pass over a
+    // zero-padded list, split between the two halves of the wavefront. The k of rank < k place themselves; their
+    // weights (wave_topk's arithmetic) are computed after the gate_up loads have been issued.
     static_assert(kFusedMaxK <= 8, "");
     if (wv == 0) {
-        float v[EJ];
         uint32_t k32[EJ];
         bool valid[EJ];
 #pragma unroll
         for (int j = 0; j < EJ; j++) {
             const int idx = lane + 64 * j;
             valid[j] = idx < E;
-            const float lv = valid[j] ? lds_logits[idx] : -INFINITY;
-            v[j] = lv == lv ? lv : -INFINITY;
-            k32[j] = valid[j] ? order_key(v[j]) : 0u;  // 0: below every logit's
+            k32[j] = valid[j] ? lds_key[idx] : 0u;  // 0: below every logit's
         }
         if (lane < 32) lds_cand[lane] = 0;  // below every candidate's key
         const int ng = (E + 31) / 32;
@@ -457,16 +488,21 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             above[q] = 0;
         }
         if (n_cand <= 32) {
-            int above1 = 0;  // two counts, so the compares do not form one dependent chain
+            // lane l and lane l + 32 both rank candidate l (l < 32), against list entries 0..15 and 16..31; the
+            // two counts meet in one v_permlane32_swap (each lane gets its partner's, and adds its own)
+            const int half = lane >> 5;
+            const uint64_t mine = lds_cand[lane & 31];
+            int c0 = 0, c1 = 0;  // two counts, so the compares do not form one dependent chain
 #pragma unroll
-            for (int u = 0; u < 32; u += 2) {
-                const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u]);
+            for (int u = 0; u < 16; u += 2) {
+                const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[16 * half + u]);
                 const uint64_t o0 = (static_cast<uint64_t>(r.y) << 32) | r.x;
                 const uint64_t o1 = (static_cast<uint64_t>(r.w) << 32) | r.z;
-                above[0] += o0 > ck[0] ? 1 : 0;
-                above1 += o1 > ck[0] ? 1 : 0;
+                c0 += o0 > mine ? 1 : 0;
+                c1 += o1 > mine ? 1 : 0;
             }
-            above[0] += above1;
+            const auto sw = __builtin_amdgcn_permlane32_swap(c0 + c1, c0 + c1, false, false);
+            above[0] = static_cast<int>(sw[0]) + static_cast<int>(sw[1]);
         } else {
             for (int u0 = 0; u0 < n_cand; u0 += 2) {  // entries past n_cand (< kFusedMaxE) are never counted
                 const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[u0]);
