@@ -104,6 +104,18 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
+// Q4_K's scales and mins of the two sub-blocks j0 and j0 + 1 (j0 even) as bytes 0 and 1 of sc2 and m2: the 6-bit
+// fields of gguf/quants.py:73-80 for both at once, with per-lane shifts instead of a branch on j0 < 4.
+__device__ __forceinline__ void q4k_scale_min2(int j0, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc2,
+                                               uint32_t& m2) {
+    const uint32_t sh = 8 * (j0 & 3);
+    const bool upper = j0 >= 4;
+    const uint32_t a = s0 >> sh, b = s1 >> sh, c = s2 >> sh;
+    const uint32_t t = upper ? 2u : 0u;
+    sc2 = ((upper ? c : a) & 0x0F0Fu) | ((a >> t) & 0x3030u);
+    m2 = ((upper ? c >> 4 : b) & 0x0F0Fu) | ((b >> t) & 0x3030u);
+}
+
 // blk: 16-byte-aligned Q4_K block.
 __device__ __forceinline__ void decode_q4k(const uint8_t* __restrict__ blk, int c, Lane32& o) {
     const uint4 hd = *reinterpret_cast<const uint4*>(blk);
@@ -169,14 +181,12 @@ struct RawLane<WL_TYPE_Q4_K> {
     }
     __device__ __forceinline__ void unpack(int c, Lane32& o) const {
         const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
-        const int j0 = 2 * (c >> 1);
-        uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(j0, hd.y, hd.z, hd.w, sc0, m0);
-        q4k_scale_min(j0 + 1, hd.y, hd.z, hd.w, sc1, m1);
-        o.a_lo = d * static_cast<float>(sc0);
-        o.b_lo = -(dmin * static_cast<float>(m0));
-        o.a_hi = d * static_cast<float>(sc1);
-        o.b_hi = -(dmin * static_cast<float>(m1));
+        uint32_t sc2, m2;
+        q4k_scale_min2(2 * (c >> 1), hd.y, hd.z, hd.w, sc2, m2);
+        o.a_lo = d * ubyte(sc2, 0);
+        o.b_lo = -(dmin * ubyte(m2, 0));
+        o.a_hi = d * ubyte(sc2, 1);
+        o.b_hi = -(dmin * ubyte(m2, 1));
         const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {

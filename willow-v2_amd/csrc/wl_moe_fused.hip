@@ -308,7 +308,9 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     const bool gu_lane = gi < nb;
     const int lo_gu = gi * kQK + BlockInfo<GU>::lo_start(c), hi_gu = lo_gu + BlockInfo<GU>::hi_offset;
     const int64_t gu_rs = static_cast<int64_t>(nb) * BlockInfo<GU>::bytes;
-    float4 xl[4], xh[4];  // loaded now; their sums are taken where they are used, so nothing waits for x here
+    // loaded now; their run sums are taken where they are first used (phase A's shared gate_up task, and once
+    // before phase B for both of its tasks), so nothing waits for x here
+    float4 xl[4], xh[4];
     if (gu_lane) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -316,15 +318,17 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             xh[i] = xload(hi_gu / 4 + i);
         }
     }
-    auto gate_up_dots = [&](const Lane32& lg, const Lane32& lu, float& g, float& u) {
+    auto gate_up_dots_s = [&](const Lane32& lg, const Lane32& lu, float sxl, float sxh, float& g, float& u) {
         float ag = 0.0f, au = 0.0f;
         if (gu_lane) {
-            const float sxl = sum16(xl), sxh = sum16(xh);
             ag = lane_dot_s(lg, xl, xh, sxl, sxh);
             au = lane_dot_s(lu, xl, xh, sxl, sxh);
         }
         g = group_sum<64>(ag);
         u = group_sum<64>(au);
+    };
+    auto gate_up_dots = [&](const Lane32& lg, const Lane32& lu, float& g, float& u) {
+        gate_up_dots_s(lg, lu, gu_lane ? sum16(xl) : 0.0f, gu_lane ? sum16(xh) : 0.0f, g, u);
     };
 
     // workgroup b < H / kOwnRows owns output rows kOwnRows b .. + kOwnRows - 1; wavefront w < 8 / R takes rows
@@ -621,7 +625,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if ((lane % WIDTH) == 0) lds_sh[R * wv + drow] = v;
     }
 
-    // gate_up: decode, dot, publish h[s][j]
+    // gate_up: decode, dot, publish h[s][j] (x's run sums once for the wavefront's tasks)
+    const float sxl = gu_lane ? sum16(xl) : 0.0f, sxh = gu_lane ? sum16(xh) : 0.0f;
 #pragma unroll
     for (int q = 0; q < kGateUpTasks; q++) {
         const int u = slot + q * NW;
@@ -632,7 +637,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
                 graw[q][1].unpack(c, lu);
             }
             float g, up;
-            gate_up_dots(lg, lu, g, up);
+            gate_up_dots_s(lg, lu, sxl, sxh, g, up);
             if (lane == 0 && publish) put_tagged(a.sync, kTagH + 2 * u, tag, silu(g) * up);  // u = s * I + j
         }
     }
