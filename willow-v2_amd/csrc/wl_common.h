@@ -170,6 +170,30 @@ __device__ __forceinline__ void decode(const uint8_t* __restrict__ blk, int c, L
 
 // decode() split in two: fetch() only issues the lane's loads (raw words kept as loaded), unpack() does the
 // arithmetic later, so code placed between them does not wait for the loads. unpack(fetch(b)) == decode(b).
+typedef _Float16 wl_f16x2 __attribute__((ext_vector_type(2)));
+
+// dot16 of a Q4_K lane's run from its raw qs dwords q[4], scaled: each nibble is read in place as the mantissa of an
+// f16 subnormal (exponent bits zero) and each product is a v_fma_mix_f32, which takes the f16 half directly, so no
+// conversion instruction is spent per value. The low nibbles (bits 0..3 of a half: value q 2^-24) give the low
+// run times 2^-24, the high nibbles (bits 4..7: q 2^-20) the high run times 2^-20. Every partial sum is dot16's
+// times that power of two exactly (normal floats; power-of-two scaling rounds the same), so with the scale
+// multiplied back (exact) the lane's sum is dot16's bit for bit.
+template <bool HIGH>
+__device__ __forceinline__ float dot16_q4mix(const uint32_t q[4], const float4 x[4]) {
+    constexpr uint32_t m = HIGH ? 0x00F000F0u : 0x000F000Fu;
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const wl_f16x2 e = __builtin_bit_cast(wl_f16x2, q[i] & m);         // bytes 0, 2
+        const wl_f16x2 o = __builtin_bit_cast(wl_f16x2, (q[i] >> 8) & m);  // bytes 1, 3
+        s0 = __builtin_fmaf(static_cast<float>(e.x), x[i].x, s0);
+        s1 = __builtin_fmaf(static_cast<float>(o.x), x[i].y, s1);
+        s0 = __builtin_fmaf(static_cast<float>(e.y), x[i].z, s0);
+        s1 = __builtin_fmaf(static_cast<float>(o.y), x[i].w, s1);
+    }
+    return s0 + s1;
+}
+
 template <int TYPE>
 struct RawLane;
 template <>
@@ -194,7 +218,28 @@ struct RawLane<WL_TYPE_Q4_K> {
             o.hi[i] = opaque((q[i] >> 4) & 0x0F0F0F0Fu);
         }
     }
+    // for lane_dot_q4mix: the raw qs dwords in lo, the low run's scale times 2^24, the high run's times 2^20
+    __device__ __forceinline__ void unpack_mix(int c, Lane32& o) const {
+        const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
+        uint32_t sc2, m2;
+        q4k_scale_min2(2 * (c >> 1), hd.y, hd.z, hd.w, sc2, m2);
+        o.a_lo = (d * 16777216.0f) * ubyte(sc2, 0);
+        o.b_lo = -(dmin * ubyte(m2, 0));
+        o.a_hi = (d * 1048576.0f) * ubyte(sc2, 1);
+        o.b_hi = -(dmin * ubyte(m2, 1));
+        o.lo[0] = qv.x;
+        o.lo[1] = qv.y;
+        o.lo[2] = qv.z;
+        o.lo[3] = qv.w;
+    }
 };
+
+// lane_dot_s for a Q4_K lane unpacked by unpack_mix (the same bits)
+__device__ __forceinline__ float lane_dot_q4mix(const Lane32& w, const float4 xl[4], const float4 xh[4], float sxl,
+                                                float sxh) {
+    return w.a_lo * dot16_q4mix<false>(w.lo, xl) + w.b_lo * sxl + w.a_hi * dot16_q4mix<true>(w.lo, xh) +
+           w.b_hi * sxh;
+}
 template <>
 struct RawLane<WL_TYPE_Q6_K> {
     uint32_t l[5], h[5];  // the aligned dwords around the lane's 16 ql and 16 qh bytes

@@ -625,7 +625,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if ((lane % WIDTH) == 0) lds_sh[R * wv + drow] = v;
     }
 
-    // gate_up: decode, dot, publish h[s][j] (x's run sums once for the wavefront's tasks)
+    // gate_up: decode, dot, publish h[s][j] (x's run sums once for the wavefront's tasks; the nibbles go into
+    // v_fma_mix_f32 products as f16 subnormals, lane_dot_q4mix)
     const float sxl = gu_lane ? sum16(xl) : 0.0f, sxh = gu_lane ? sum16(xh) : 0.0f;
 #pragma unroll
     for (int q = 0; q < kGateUpTasks; q++) {
@@ -633,11 +634,16 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if (u < n_tasks) {
             Lane32 lg, lu;
             if (gu_lane) {
-                graw[q][0].unpack(c, lg);
-                graw[q][1].unpack(c, lu);
+                graw[q][0].unpack_mix(c, lg);
+                graw[q][1].unpack_mix(c, lu);
             }
-            float g, up;
-            gate_up_dots_s(lg, lu, sxl, sxh, g, up);
+            float g = 0.0f, up = 0.0f;
+            if (gu_lane) {
+                g = lane_dot_q4mix(lg, xl, xh, sxl, sxh);
+                up = lane_dot_q4mix(lu, xl, xh, sxl, sxh);
+            }
+            g = group_sum<64>(g);
+            up = group_sum<64>(up);
             if (lane == 0 && publish) put_tagged(a.sync, kTagH + 2 * u, tag, silu(g) * up);  // u = s * I + j
         }
     }
