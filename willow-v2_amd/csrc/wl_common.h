@@ -329,6 +329,19 @@ __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// v plus its partner's v across 16-lane rows (XOR 16: ROWS = 16) or wavefront halves (XOR 32: ROWS = 32), in one
+// VALU swap: v_permlane16_swap / v_permlane32_swap with both operands v give every lane its own v and its
+// partner's, one in each result, and their sum (addition commutes exactly) is v + v[lane ^ ROWS] bit for bit, with
+// no trip through the LDS crossbar that a shuffle takes.
+template <int ROWS>
+__device__ __forceinline__ float swap_add(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = ROWS == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                              : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 // Sum over aligned groups of WIDTH lanes (2..64); every lane of a group gets the same bits. Must be called with
 // the whole wavefront active.
 template <int WIDTH>
@@ -337,8 +350,8 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (WIDTH >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (WIDTH >= 8) v += dpp<0x141>(v);  // row_half_mirror: the other quad of the 8
     if constexpr (WIDTH >= 16) v += dpp<0x140>(v); // row_mirror: the other 8 of the 16
-    if constexpr (WIDTH >= 32) v += __shfl_xor(v, 16);
-    if constexpr (WIDTH >= 64) v += __shfl_xor(v, 32);
+    if constexpr (WIDTH >= 32) v = swap_add<16>(v);
+    if constexpr (WIDTH >= 64) v = swap_add<32>(v);
     return v;
 }
 
