@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const float* __restrict__ x
 struct Q4KRowState {
     uint4 hd;       // d, dmin, 12 scale bytes
     uint4 qs[2];    // qs bytes 32 q .. 32 q + 31
-    float a[2], b[2];  // value = a[e] * nibble + b[e] for sub-block 2 q + e
+    float a[2], b[2];  // value = a[e] * nibble + b[e] for sub-block 2 q + e, a[e] scaled for fragment_q4k
 };
 
 __device__ __forceinline__ void fetch_q4k(const uint8_t* __restrict__ blk, int q, Q4KRowState& s) {
@@ -248,22 +248,19 @@ __device__ __forceinline__ void prepare_q4k(Q4KRowState& s, int q) {
         const uint32_t s0 = s.hd.y >> sh, s1 = s.hd.z >> sh, s2 = s.hd.w >> sh;
         const uint32_t sc = ((s0 >> sh_hi) & mask_top) | (s2 & mask_low);
         const uint32_t m = ((s1 >> sh_hi) & mask_top) | ((s2 >> 4) & mask_low);
-        s.a[e] = d * static_cast<float>(sc);
+        // times 2^24 for the low nibbles, 2^20 for the high ones: the f16-subnormal scale of fragment_q4k (exact)
+        s.a[e] = (d * (e ? 1048576.0f : 16777216.0f)) * static_cast<float>(sc);
         s.b[e] = -(dmin * static_cast<float>(m));
     }
 }
 
-// v & 0x0F0F0F0F as an opaque value, so the byte conversions below stay single v_cvt_f32_ubyteN instructions
-__device__ __forceinline__ uint32_t nibbles(uint32_t v) {
-    uint32_t r;
-    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-
-// 4 bytes of w (values 0..255) as bf16 of a * q + b, packed two per dword
-__device__ __forceinline__ void affine4(uint32_t w, float a, float b, uint32_t& p0, uint32_t& p1) {
-    p0 = pack2(__builtin_fmaf(a, ubyte(w, 0), b), __builtin_fmaf(a, ubyte(w, 1), b));
-    p1 = pack2(__builtin_fmaf(a, ubyte(w, 2), b), __builtin_fmaf(a, ubyte(w, 3), b));
+// 4 values as f16 subnormals (values 0 and 2 in the halves of e, 1 and 3 in those of o; a half with zero exponent
+// bits and mantissa q is q 2^-k) as bf16 of a * q + b, packed two per dword: each a v_fma_mix_f32 that reads the half
+// directly (no conversion instruction per value), with a scaled by 2^k (exact), so a * q is the same exact product
+__device__ __forceinline__ void affine4_h(uint32_t e, uint32_t o, float a, float b, uint32_t& p0, uint32_t& p1) {
+    const wl_f16x2 he = __builtin_bit_cast(wl_f16x2, e), ho = __builtin_bit_cast(wl_f16x2, o);
+    p0 = pack2(__builtin_fmaf(a, static_cast<float>(he.x), b), __builtin_fmaf(a, static_cast<float>(ho.x), b));
+    p1 = pack2(__builtin_fmaf(a, static_cast<float>(he.y), b), __builtin_fmaf(a, static_cast<float>(ho.y), b));
 }
 
 template <int KK>
@@ -271,11 +268,11 @@ __device__ __forceinline__ bf16x8 fragment_q4k(const Q4KRowState& s) {
     constexpr int e = KK & 1, j = KK >> 1;  // sub-block 2 q + e, its bytes 8 j .. 8 j + 7
     const uint4 w = s.qs[j >> 1];
     const uint32_t w0 = (j & 1) ? w.z : w.x, w1 = (j & 1) ? w.w : w.y;
-    constexpr uint32_t sh = 4 * e;
-    const uint32_t lo = nibbles(w0 >> sh), hi = nibbles(w1 >> sh);
+    // the nibbles in place as f16 subnormals: low ones (bits 0..3 of a half) q 2^-24, high ones (bits 4..7) q 2^-20
+    constexpr uint32_t m = e ? 0x00F000F0u : 0x000F000Fu;
     uint4 p;
-    affine4(lo, s.a[e], s.b[e], p.x, p.y);
-    affine4(hi, s.a[e], s.b[e], p.z, p.w);
+    affine4_h(w0 & m, (w0 >> 8) & m, s.a[e], s.b[e], p.x, p.y);
+    affine4_h(w1 & m, (w1 >> 8) & m, s.a[e], s.b[e], p.z, p.w);
     return __builtin_bit_cast(bf16x8, p);
 }
 
@@ -334,8 +331,9 @@ __device__ __forceinline__ bf16x8 fragment_q6k(const Q6KRowState& s) {
     const float b = -32.0f * a;  // exact: a has at most 19 significant bits
     // a * (q - 32) == fma(a, q, -32 a): the product a * q is exact, so both round the same sum once
     uint4 p;
-    affine4(v0, a, b, p.x, p.y);
-    affine4(v1, a, b, p.z, p.w);
+    const float a24 = a * 16777216.0f;  // the bytes as f16 subnormals (q 2^-24), exact
+    affine4_h(v0 & 0x00FF00FFu, (v0 >> 8) & 0x00FF00FFu, a24, b, p.x, p.y);
+    affine4_h(v1 & 0x00FF00FFu, (v1 >> 8) & 0x00FF00FFu, a24, b, p.z, p.w);
     return __builtin_bit_cast(bf16x8, p);
 }
 
