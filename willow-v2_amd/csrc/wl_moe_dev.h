@@ -77,9 +77,15 @@ __device__ __forceinline__ float router_row_xw(XF x4, WF w4, bool valid, int H, 
         float p = 0.0f;
         const int s = slot + 32 * j;
         if (valid && s < nseg) {
+            // the segment's x requested before the chain starts (all 16 loads in flight; interleaved with the
+            // chain by the scheduler, two were, and each group of four FMAs waited out a load)
+            float4 xs[kRouterSeg / 4];
+#pragma unroll
+            for (int i = 0; i < kRouterSeg / 4; i++) xs[i] = x4(s * (kRouterSeg / 4) + i);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < kRouterSeg / 4; i++) {
-                const float4 wv = w4(s, i), xv = x4(s * (kRouterSeg / 4) + i);
+                const float4 wv = w4(s, i), xv = xs[i];
                 p = __builtin_fmaf(xv.x, wv.x, p);
                 p = __builtin_fmaf(xv.y, wv.y, p);
                 p = __builtin_fmaf(xv.z, wv.z, p);
@@ -90,6 +96,9 @@ __device__ __forceinline__ float router_row_xw(XF x4, WF w4, bool valid, int H, 
         float parts[32];
 #pragma unroll
         for (int sl = 0; sl < 32; sl++) parts[sl] = __shfl(p, src_base + sl);
+        // every shuffle issued before the first add (left to the scheduler, each add waited for its shuffle with
+        // two more in flight: 32 LDS round trips a third at a time)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int sl = 0; sl < 32; sl++) {
             const int sg = sl + 32 * j;
