@@ -114,7 +114,8 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
 
 // Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset), handing each to
 // put(i, value) once it carries `tag` (workgroup-cooperative: thread t polls values t + q blockDim.x, q < Q;
-// n <= Q blockDim.x); false if spin_limit polls pass first. Two polling rounds are in flight: a round's loads are
+// n <= Q blockDim.x); false if spin_limit polls pass first. lds_bad: an LDS word that is 0 on entry; a thread that
+// gave up sets it, and after one barrier every thread reads the verdict (__syncthreads_and takes three). Two polling rounds are in flight: a round's loads are
 // issued before the previous round's are checked, so a value is seen about half a load's round trip after it
 // lands instead of a whole one (the logits exchange of the b=1 decode: 15.88 -> 15.62 us per layer; three or four
 // rounds in flight measured slower, their extra loads queueing at the few lines every workgroup polls). Every
@@ -122,7 +123,7 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
 // so a round's loads are unconditional and the compiler keeps the older round outstanding while it checks.
 template <int Q, typename Src, typename Put>
 __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit, Src src,
-                                              Put put) {
+                                              Put put, uint32_t* lds_bad) {
     const uint64_t* w[Q];
     bool pend[Q];
 #pragma unroll
@@ -161,7 +162,9 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
         check(rb);
         if (!waiting()) break;
     }
-    return __syncthreads_and(!waiting());
+    if (waiting()) *lds_bad = 1u;
+    __syncthreads();
+    return *lds_bad == 0u;
 }
 
 // The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. It first waits on the last
@@ -215,6 +218,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ uint32_t lds_key[kFusedMaxE];        // the expert logits' order keys (NaN as -inf)
     __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
+    __shared__ uint32_t lds_bad[2];  // a wait gave up: the routing gather's, the call's
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
     // x (NORM: normalized) for every read, 4 floats of padding after every 64 values (x_slot)
     __shared__ __attribute__((aligned(16))) float lds_xn[kFusedMaxHidden + kFusedMaxHidden / 16];
@@ -406,6 +410,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // each expert logit lands, its order key (NaN as -inf) goes to lds_key and into its 32-logit group's maximum,
     // which the top-k below needs: the keys and maxima are formed while the gather waits, not after it.
     if (threadIdx.x < kFusedMaxE / 32) lds_gmax[threadIdx.x] = 0u;
+    if (threadIdx.x < 2) lds_bad[threadIdx.x] = 0u;
     __syncthreads();
     {
         const int n_route = n_logits + (shared ? I : 0);
@@ -423,8 +428,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         };
         static_assert(3 * kFusedThreads >= kFusedMaxE + 1 + kFusedMaxInter, "three values per thread at most");
-        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put)
-                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put)) &&
+        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put, &lds_bad[0])
+                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put, &lds_bad[0])) &&
              ok;
     }
     // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
@@ -720,12 +725,24 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     }
 
     // combine: the owner's rows y[j] = sum_s w_s P[s][j] (+ sg * shared), s in ascending expert id
-    const bool all_ok = __syncthreads_and(ok);
+    // every wait of the call ended (one barrier and a flag word instead of __syncthreads_and's three barriers)
+    if (!ok) lds_bad[1] = 1u;
+    __syncthreads();
+    const bool all_ok = lds_bad[1] == 0u;
     if (owner && threadIdx.x < kOwnRows) {
         const int r = threadIdx.x;
+        // every weight and partial read before the chain (a loop over kk waited out one LDS read per term)
+        float wv[kFusedMaxK], pv[kFusedMaxK];
+#pragma unroll
+        for (int s = 0; s < kFusedMaxK; s++) {
+            wv[s] = lds_wsel[s];
+            pv[s] = lds_p[s * kOwnRows + r];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         float acc = 0.0f;
-        for (int s = 0; s < kk; s++)
-            acc = s == 0 ? lds_wsel[s] * lds_p[r] : acc + lds_wsel[s] * lds_p[s * kOwnRows + r];
+#pragma unroll
+        for (int s = 0; s < kFusedMaxK; s++)
+            if (s < kk) acc = s == 0 ? wv[s] * pv[s] : acc + wv[s] * pv[s];
         if (shared) acc = acc + sgv * lds_sh[r];
         if (a.residual) acc = __fadd_rn(a.x[kOwnRows * b + r], acc);
         a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
