@@ -161,15 +161,14 @@ __device__ __forceinline__ void softmax_stats(const float* __restrict__ lt, int 
 // softmax_stats' sum s for a known max m (bitwise the same: per lane in j order, then across the wave).
 template <int EJ>
 __device__ __forceinline__ float softmax_sum(const float* __restrict__ lt, int E, int lane, float m) {
+    float lv[EJ];  // every read issued before the first use (read under the branch, each waited out its own)
+#pragma unroll
+    for (int j = 0; j < EJ; j++) lv[j] = lt[lane + 64 * j < E ? lane + 64 * j : 0];
+    __builtin_amdgcn_sched_barrier(0);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < EJ; j++) {
-        const int idx = lane + 64 * j;
-        if (idx < E) {
-            const float lv = lt[idx];
-            s += expf((lv == lv ? lv : -INFINITY) - m);
-        }
-    }
+    for (int j = 0; j < EJ; j++)
+        if (lane + 64 * j < E) s += expf((lv[j] == lv[j] ? lv[j] : -INFINITY) - m);
     return group_sum<64>(s);
 }
 

@@ -466,7 +466,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         for (int j = 0; j < EJ; j++) {
             const int idx = lane + 64 * j;
             valid[j] = idx < E;
-            k32[j] = valid[j] ? lds_key[idx] : 0u;  // 0: below every logit's
+            k32[j] = lds_key[valid[j] ? idx : 0];  // unconditional, so the reads are in flight together
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < EJ; j++) {
+            if (!valid[j]) k32[j] = 0u;  // 0: below every logit's
         }
         if (lane < 32) lds_cand[lane] = 0;  // below every candidate's key
         const int ng = (E + 31) / 32;
@@ -502,9 +507,13 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             const int half = lane >> 5;
             const uint64_t mine = lds_cand[lane & 31];
             int c0 = 0, c1 = 0;  // two counts, so the compares do not form one dependent chain
+            uint4 rr[8];  // the 8 list reads in flight at once, then the compares
+#pragma unroll
+            for (int u = 0; u < 16; u += 2) rr[u / 2] = *reinterpret_cast<const uint4*>(&lds_cand[16 * half + u]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < 16; u += 2) {
-                const uint4 r = *reinterpret_cast<const uint4*>(&lds_cand[16 * half + u]);
+                const uint4 r = rr[u / 2];
                 const uint64_t o0 = (static_cast<uint64_t>(r.y) << 32) | r.x;
                 const uint64_t o1 = (static_cast<uint64_t>(r.w) << 32) | r.z;
                 c0 += o0 > mine ? 1 : 0;
