@@ -115,12 +115,13 @@ __device__ __forceinline__ void put_tagged(uint32_t* sync_base, int word, uint32
 // Gathers n tagged values (value i: the 64-bit word at sync + src(i), a 32-bit word offset), handing each to
 // put(i, value) once it carries `tag` (workgroup-cooperative: thread t polls values t + q blockDim.x, q < Q;
 // n <= Q blockDim.x); false if spin_limit polls pass first. lds_bad: an LDS word that is 0 on entry; a thread that
-// gave up sets it, and after one barrier every thread reads the verdict (__syncthreads_and takes three). Two polling rounds are in flight: a round's loads are
-// issued before the previous round's are checked, so a value is seen about half a load's round trip after it
-// lands instead of a whole one (the logits exchange of the b=1 decode: 15.88 -> 15.62 us per layer; three or four
-// rounds in flight measured slower, their extra loads queueing at the few lines every workgroup polls). Every
-// slot is loaded in every round (a value already in, or an index past n, reloads a word whose result is dropped),
-// so a round's loads are unconditional and the compiler keeps the older round outstanding while it checks.
+// gave up sets it, and after one barrier every thread reads the verdict (__syncthreads_and takes three barriers).
+// Two polling rounds are in flight: a round's loads are issued before the previous round's are checked, so a value
+// is seen about half a load's round trip after it lands instead of a whole one (the logits exchange of the b=1
+// decode: 15.88 -> 15.62 us per layer; three or four rounds in flight measured slower, their extra loads queueing
+// at the few lines every workgroup polls). Every slot is loaded in every round (a value already in, or an index
+// past n, reloads a word whose result is dropped), so a round's loads are unconditional and the compiler keeps the
+// older round outstanding while it checks.
 template <int Q, typename Src, typename Put>
 __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit, Src src,
                                               Put put, uint32_t* lds_bad) {
@@ -428,8 +429,9 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         };
         static_assert(3 * kFusedThreads >= kFusedMaxE + 1 + kFusedMaxInter, "three values per thread at most");
-        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put, &lds_bad[0])
-                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put, &lds_bad[0])) &&
+        uint32_t* bad = &lds_bad[0];
+        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put, bad)
+                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put, bad)) &&
              ok;
     }
     // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
