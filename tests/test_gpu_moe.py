@@ -246,7 +246,8 @@ def test_layer_zipf_b64(hip):
 
 
 @pytest.mark.parametrize("variant", ["no_shared", "no_shared_gate", "q4k_down", "q6k_gate_up", "topk1",
-                                     "few_experts", "hidden_1024", "inter_256_no_norm"])
+                                     "few_experts", "hidden_1024", "inter_256_no_norm", "inter_1024",
+                                     "inter_1024_no_shared"])
 def test_layer_variants(hip, variant):
     kw = dict(hidden=1024, inter=512, shared_inter=512, experts=32, top_k=4)
     if variant == "q4k_down":
@@ -261,8 +262,12 @@ def test_layer_variants(hip, variant):
         kw.update(hidden=1024, experts=64, top_k=8)
     if variant == "inter_256_no_norm":
         kw.update(inter=256, shared_inter=768)
+    if variant.startswith("inter_1024"):
+        # 1024-wide experts: the fused kernel's four-block down rows; with the shared expert the routing gather
+        # takes 65 logits + 1024 shared values, more than two per thread (its three-slot form)
+        kw.update(inter=1024, shared_inter=1024, experts=64, top_k=4)
     lw = synth.moe_layer(50, **kw)
-    if variant == "no_shared":
+    if variant in ("no_shared", "inter_1024_no_shared"):
         lw["shared_gate_up"] = lw["shared_down"] = lw["shared_gate"] = None
     if variant == "no_shared_gate":
         lw["shared_gate"] = None
@@ -271,6 +276,8 @@ def test_layer_variants(hip, variant):
     layer = hip.MoELayer.from_host(lw)
     if variant == "q6k_gate_up":
         assert layer.plan(1) == "gemv"
+    if variant.startswith("inter_1024"):
+        assert layer.plan(1) == "fused"
     for T in (1, 5):
         check_layer(hip, layer, lw, synth.tokens(51 + T, T, kw["hidden"]), f"{variant}")
 
@@ -332,7 +339,7 @@ def test_prefill_mfma_variants(hip, variant):
     if variant == "inter_256":
         kw.update(inter=256, shared_inter=256)
     lw = synth.moe_layer(70, **kw)
-    if variant == "no_shared":
+    if variant in ("no_shared", "inter_1024_no_shared"):
         lw["shared_gate_up"] = lw["shared_down"] = lw["shared_gate"] = None
     layer = hip.MoELayer.from_host(lw, mfma="always")
     T = 37 if variant == "partial_tiles" else 300  # 300 * 4 / 16 = 75 tokens per expert on average
