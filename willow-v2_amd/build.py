@@ -18,7 +18,9 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
-    # no packed fp32 instructions (v_pk_*_f32) anywhere: written off on this hardware pool
+    # no packed fp32 instructions (v_pk_*_f32) anywhere: some of their forms have given wrong results on MI355X.
+    # f16 denormals must stay enabled (the default; no -fdenormal-fp-math=preserve-sign or fast-math): the
+    # dequantizing kernels feed quantized values to v_fma_mix_f32 as f16 subnormals
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
