@@ -7,7 +7,7 @@
 //             neither of which depends on the routing; each workgroup also loads the shared expert's down rows of
 //             the output rows it owns (8 per workgroup);
 //   routing   every workgroup gathers the logits and h_shared and runs the top-k itself (candidate ranks
-//             counted by the workgroup, the weights by wavefront 0);
+//             counted by the workgroup, the weights by wavefront 3);
 //   phase B   every wavefront issues the loads of its gate_up tasks (a gate row and its up row of one picked
 //             expert) at once, kept as raw words; while they are in flight the owners dot their shared down rows
 //             with h_shared; then the gate_up rows are decoded and dotted, and h (silu(g) * u) published;
@@ -606,9 +606,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             graw[q][1].fetch(w + (I + j) * gu_rs + gi * BlockInfo<GU>::bytes, c);
         }
     }
-    // the routing weights, needed only by the final sum: wavefront 0 computes them while the loads above are in flight
-    // (softmax over all logits with the max from pick 0, as softmax_stats takes it; renormalised in pick order)
-    if (wv == 0 && !(a.min_w > 0.0f)) {
+    // the routing weights, needed only by the final sum: wavefront 3 computes them while the loads above are in flight
+    // (softmax over all logits with the max from pick 0, as softmax_stats takes it; renormalised in pick order). Not
+    // wavefront 0: its SIMD has just run the top-k and runs the shared down rows next.
+    if (wv == 3 && !(a.min_w > 0.0f)) {
         const int my_id = lane < k ? lds_pick[lane] : 0;
         const float lv0 = lds_logits[__builtin_amdgcn_readfirstlane(my_id)];
         const float m = lv0 == lv0 ? lv0 : -INFINITY;
