@@ -168,6 +168,71 @@ __device__ __forceinline__ bool gather_tagged(const uint32_t* sync, int n, uint3
     return *lds_bad == 0u;
 }
 
+// The same over a share of the workgroup, thread t of nt (values t + q nt), with no barrier at the end: returns
+// whether every value of this thread arrived.
+template <int Q, typename Src, typename Put>
+__device__ __forceinline__ bool gather_tagged_part(const uint32_t* sync, int n, uint32_t tag, uint32_t spin_limit,
+                                                   Src src, Put put, int t, int nt) {
+    const uint64_t* w[Q];
+    bool pend[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int i = t + q * nt;
+        pend[q] = i < n;
+        w[q] = reinterpret_cast<const uint64_t*>(sync + src(pend[q] ? i : 0));
+    }
+    auto ld = [](const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto waiting = [&] {
+        bool r = false;
+#pragma unroll
+        for (int q = 0; q < Q; q++) r = r || pend[q];
+        return r;
+    };
+    auto check = [&](const uint64_t (&v)[Q]) {
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (pend[q] && static_cast<uint32_t>(v[q] >> 32) == tag) {
+                put(t + q * nt, __builtin_bit_cast(float, static_cast<uint32_t>(v[q])));
+                pend[q] = false;
+            }
+    };
+    uint64_t ra[Q], rb[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) ra[q] = ld(w[q]);
+    for (uint32_t spins = 0; spins <= spin_limit; spins += 2) {
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 0; q < Q; q++) rb[q] = ld(w[q]);
+        check(ra);
+        if (!waiting()) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int q = 0; q < Q; q++) ra[q] = ld(w[q]);
+        check(rb);
+        if (!waiting()) break;
+    }
+    return !waiting();
+}
+
+// The expert logits for the top-k, gathered by its wavefront alone: lane l polls logits l + 64 j (j < EJ, those
+// below E), writes each to lds_logits as it lands and keeps its order key (NaN as -inf; 0 for an index past E, or
+// for a logit that never arrived) in key[j]. Returns whether every one of the lane's logits arrived.
+template <int EJ>
+__device__ __forceinline__ bool gather_logits_wave(const uint32_t* sync, int E, uint32_t tag, uint32_t spin_limit,
+                                                   float* lds_logits, uint32_t (&key)[EJ]) {
+    const int lane = threadIdx.x & 63;
+    auto put = [&](int i, float v) {
+        lds_logits[i] = v;
+        const int j = (i - lane) >> 6;
+#pragma unroll
+        for (int jj = 0; jj < EJ; jj++)
+            if (jj == j) key[jj] = order_key(v == v ? v : -INFINITY);
+    };
+#pragma unroll
+    for (int j = 0; j < EJ; j++) key[j] = 0u;
+    return gather_tagged_part<EJ>(sync, E, tag, spin_limit, [&](int i) { return kTagLogits + 2 * i; }, put, lane, 64);
+}
+
 // The same for one wavefront alone: n = 64 Q values, lane l polling values l + 64 q. It first waits on the last
 // value of each lane only (64 words instead of 64 Q per round), then gathers them all: an expert's last h values
 // come from the highest-numbered workgroups, which start last, so by the time those are in, nearly all of them
@@ -216,8 +281,6 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
-    __shared__ uint32_t lds_key[kFusedMaxE];        // the expert logits' order keys (NaN as -inf)
-    __shared__ uint32_t lds_gmax[kFusedMaxE / 32];  // each 32-logit group's largest order key (0: none yet)
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ uint32_t lds_bad[2];  // a wait gave up: the routing gather's, the call's
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
@@ -406,32 +469,32 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
     }
 
-    // routing: the logits and h_shared (both from phase A) in one gather, then the top-k. The barrier keeps the
-    // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading. As
-    // each expert logit lands, its order key (NaN as -inf) goes to lds_key and into its 32-logit group's maximum,
-    // which the top-k below needs: the keys and maxima are formed while the gather waits, not after it.
-    if (threadIdx.x < kFusedMaxE / 32) lds_gmax[threadIdx.x] = 0u;
+    // routing: the logits and h_shared (both from phase A) gathered, then the top-k. The barrier keeps the
+    // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading; the
+    // barrier after the top-k is the one that makes the gathered values visible to every wavefront.
     if (threadIdx.x < 2) lds_bad[threadIdx.x] = 0u;
     __syncthreads();
-    {
-        const int n_route = n_logits + (shared ? I : 0);
-        auto src = [&](int i) { return i < n_logits ? kTagLogits + 2 * i : kTagHsh + 2 * (i - n_logits); };
+    // wavefront 0 gathers the expert logits into registers for the top-k (the keys need no LDS round trip and no
+    // barrier before it); the other wavefronts gather the rest: the shared gate's logit and h_shared
+    uint32_t k32[EJ];
+    if (wv == 0) {
+        ok = gather_logits_wave<EJ>(a.sync, E, tag, a.spin_limit, lds_logits, k32) && ok;
+        lane_sync();  // its lds_logits writes before any lane's reads below
+    } else {
+        const int n_gate = n_logits - E;  // 1 with a shared gate, else 0
+        const int n_rest = n_gate + (shared ? I : 0);
+        auto src = [&](int i) { return i < n_gate ? kTagLogits + 2 * (E + i) : kTagHsh + 2 * (i - n_gate); };
         auto put = [&](int i, float v) {
-            if (i < n_logits) {
-                lds_logits[i] = v;
-                if (i < E) {
-                    const uint32_t kv = order_key(v == v ? v : -INFINITY);
-                    lds_key[i] = kv;
-                    atomicMax(&lds_gmax[i >> 5], kv);
-                }
-            } else {
-                lds_hsh[i - n_logits] = v;
-            }
+            if (i < n_gate)
+                lds_logits[E + i] = v;
+            else
+                lds_hsh[i - n_gate] = v;
         };
-        static_assert(3 * kFusedThreads >= kFusedMaxE + 1 + kFusedMaxInter, "three values per thread at most");
-        uint32_t* bad = &lds_bad[0];
-        ok = (n_route <= 2 * kFusedThreads ? gather_tagged<2>(a.sync, n_route, tag, a.spin_limit, src, put, bad)
-                                           : gather_tagged<3>(a.sync, n_route, tag, a.spin_limit, src, put, bad)) &&
+        constexpr int nt = kFusedThreads - 64;
+        static_assert(3 * nt >= 1 + kFusedMaxInter, "three values per thread at most");
+        const int t = static_cast<int>(threadIdx.x) - 64;
+        ok = (n_rest <= 2 * nt ? gather_tagged_part<2>(a.sync, n_rest, tag, a.spin_limit, src, put, t, nt)
+                               : gather_tagged_part<3>(a.sync, n_rest, tag, a.spin_limit, src, put, t, nt)) &&
              ok;
     }
     // the guessed experts' gate_up rows this workgroup reads below (its gate_up task u = s I + j sits on wavefront
@@ -452,8 +515,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
             }
         }
     }
-    // top-k, in wavefront 0. Lane l holds the order keys of logits l + 64 j (lds_key, written by the gather). The
-    // groups of 32 logits (i / 32) have their largest order key in lds_gmax (formed during the gather); with T0 the
+    // top-k, in wavefront 0. Lane l holds the order keys of logits l + 64 j (k32, from its gather). The groups of 32
+    // logits (i / 32) have their largest order key formed in registers (a half-wavefront maximum); with T0 the
     // smallest maximum of the groups that hold a logit, at least that many keys are >= T0, so when those are at
     // least k the top k are among the candidates key >= T0 (typically 8 to 25), otherwise every logit is one. The
     // candidates (key: order key, then inverted id; 64 bits, all distinct: larger first, ties to the lower id) are
@@ -462,25 +525,25 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // weights (wave_topk's arithmetic) are computed after the gate_up loads have been issued.
     static_assert(kFusedMaxK <= 8, "");
     if (wv == 0) {
-        uint32_t k32[EJ];
         bool valid[EJ];
 #pragma unroll
-        for (int j = 0; j < EJ; j++) {
-            const int idx = lane + 64 * j;
-            valid[j] = idx < E;
-            k32[j] = lds_key[valid[j] ? idx : 0];  // unconditional, so the reads are in flight together
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < EJ; j++) {
-            if (!valid[j]) k32[j] = 0u;  // 0: below every logit's
-        }
+        for (int j = 0; j < EJ; j++) valid[j] = lane + 64 * j < E;  // k32[j] is 0 where not: below every logit's
         if (lane < 32) lds_cand[lane] = 0;  // below every candidate's key
+        // each 32-logit group's largest key: group 2 j + (l >> 5) is held by half l >> 5 of the wavefront at j
         const int ng = (E + 31) / 32;
         uint32_t t0 = 0xFFFFFFFFu;
 #pragma unroll
-        for (int g = 0; g < 2 * EJ; g++)  // the same word for every lane (a broadcast read)
-            if (g < ng) t0 = min(t0, lds_gmax[g]);
+        for (int j = 0; j < EJ; j++) {
+            uint32_t g = k32[j];
+            g = max(g, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(g), 0xB1, 0xF, 0xF, false)));
+            g = max(g, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(g), 0x4E, 0xF, 0xF, false)));
+            g = max(g, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(g), 0x141, 0xF, 0xF, false)));
+            g = max(g, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(g), 0x140, 0xF, 0xF, false)));
+            const auto sw = __builtin_amdgcn_permlane16_swap(g, g, false, false);
+            g = max(static_cast<uint32_t>(sw[0]), static_cast<uint32_t>(sw[1]));
+            if (2 * j < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(g), 0)));
+            if (2 * j + 1 < ng) t0 = min(t0, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(g), 32)));
+        }
         if (ng < k) t0 = 0;
         lane_sync();
         int n_cand = 0;
