@@ -249,7 +249,10 @@ class GGMLWeight:
     (gguf/metal.py:407). With keep_dense (the default) the bf16 values are dequantized once, on the first such call,
     and kept in HBM beside the blocks (2 bytes per value; the non-expert weights are a few GB at most against 288 GB),
     so each call is the same bf16 F.linear on the same values, the library GEMM alone. With keep_dense False nothing
-    is kept: wl_linear runs the product with the weights dequantized in registers (no bf16 copy, slower)."""
+    is kept between calls: each call is the reference's own form, the weight dequantized to a bf16 temporary and
+    the library GEMM on it (bit for bit the reference's arithmetic). linear_mfma (wl_linear, the weights dequantized
+    in registers, no temporary) is the form for a caller that cannot hold the temporary; on dense shapes it is the
+    slower one at every token count measured from 16 to 8192."""
 
     keep_dense = True
 
@@ -299,9 +302,7 @@ class GGMLWeight:
             y = gemv(self.raw, self.type_name, self.shape, flat).to(x.dtype)
         elif self.keep_dense:  # the reference's arithmetic (gguf/metal.py:407) on bf16 values kept in HBM
             y = F.linear(flat.to(torch.bfloat16), self.dense()).to(x.dtype)
-        elif self.shape[0] % 256 == 0 and self.shape[1] % 256 == 0:
-            y = linear_mfma(self.raw, self.type_name, self.shape, flat).to(x.dtype)
-        else:  # the reference's own form (gguf/metal.py:407)
+        else:  # the reference's own form (gguf/metal.py:407): dequantized on every call, nothing kept
             y = F.linear(flat.to(torch.bfloat16), dequantize_gpu(self.raw, self.type_name, self.shape)).to(x.dtype)
         return y.view(*x.shape[:-1], y.shape[-1]).to(x.device)
 
