@@ -886,20 +886,35 @@ struct BlockDot<WL_TYPE_Q4_K> {
                 const int j = 2 * q + e;
                 uint32_t sc, m;
                 q4k_scale_min(j, hd.y, hd.z, hd.w, sc, m);
-                const float a = d * static_cast<float>(sc), b = -(dmin * static_cast<float>(m));
-                // 16 values at a time: half the registers of converting the whole 32-value run at once (117
-                // instead of 134 VGPRs for k_gate_up<Q4_K>, four workgroups per CU instead of three)
+                const float a = (d * (e ? 1048576.0f : 16777216.0f)) * static_cast<float>(sc),
+                            b = -(dmin * static_cast<float>(m));
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
-                    float f[16];
+                    // the nibbles in place as f16 subnormals (q 2^-24 low, q 2^-20 high), a scaled to match: the
+                    // products and every rounding after them are the same as with the nibbles converted to floats
+                    const uint32_t msk = e ? 0x00F000F0u : 0x000F000Fu;
+                    uint32_t ev[4], od[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        bytes_to_f32(opaque((w[4 * hh + i] >> (4 * e)) & 0x0F0F0F0Fu), f + 4 * i);
+                    for (int i = 0; i < 4; i++) {
+                        ev[i] = opaque(w[4 * hh + i] & msk);
+                        od[i] = opaque((w[4 * hh + i] >> 8) & msk);
+                    }
 #pragma unroll
                     for (int u = 0; u < kGemvTok; u++) {
                         if (u < n) {
-                            const float* x = xs + u * ldx + 32 * j + 16 * hh;
-                            acc[u] += a * dot16_lds(f, x) + b * ss[u * lds_ + 2 * j + hh];
+                            const float4* x4 = reinterpret_cast<const float4*>(xs + u * ldx + 32 * j + 16 * hh);
+                            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                            for (int i = 0; i < 4; i++) {
+                                const float4 v = x4[i];
+                                const wl_f16x2 he = __builtin_bit_cast(wl_f16x2, ev[i]);
+                                const wl_f16x2 ho = __builtin_bit_cast(wl_f16x2, od[i]);
+                                s0 = __builtin_fmaf(static_cast<float>(he.x), v.x, s0);
+                                s1 = __builtin_fmaf(static_cast<float>(ho.x), v.y, s1);
+                                s0 = __builtin_fmaf(static_cast<float>(he.y), v.z, s0);
+                                s1 = __builtin_fmaf(static_cast<float>(ho.y), v.w, s1);
+                            }
+                            acc[u] += a * (s0 + s1) + b * ss[u * lds_ + 2 * j + hh];
                         }
                     }
                 }
