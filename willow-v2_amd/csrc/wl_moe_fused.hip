@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
-    __shared__ uint32_t lds_bad[2];  // a wait gave up: the routing gather's, the call's
+    __shared__ uint32_t lds_bad[3];  // a wait gave up: the routing gather's, the call's; wavefronts done
     __shared__ int lds_kk;  // experts run: k, or with min_w those skip_small keeps
     // x (NORM: normalized) for every read, 4 floats of padding after every 64 values (x_slot)
     __shared__ __attribute__((aligned(16))) float lds_xn[kFusedMaxHidden + kFusedMaxHidden / 16];
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     // routing: the logits and h_shared (both from phase A) gathered, then the top-k. The barrier keeps the
     // workgroup's idle wavefronts from polling while its phase A work (and everyone else's) is still loading; the
     // barrier after the top-k is the one that makes the gathered values visible to every wavefront.
-    if (threadIdx.x < 2) lds_bad[threadIdx.x] = 0u;
+    if (threadIdx.x < 3) lds_bad[threadIdx.x] = 0u;
     __syncthreads();
     // wavefront 0 gathers the expert logits into registers for the top-k (the keys need no LDS round trip and no
     // barrier before it); the other wavefronts gather the rest: the shared gate's logit and h_shared
@@ -799,13 +799,18 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         }
     }
 
-    // combine: the owner's rows y[j] = sum_s w_s P[s][j] (+ sg * shared), s in ascending expert id
-    // every wait of the call ended (one barrier and a flag word instead of __syncthreads_and's three barriers)
+    // combine: the owner's rows y[j] = sum_s w_s P[s][j] (+ sg * shared), s in ascending expert id, by the last
+    // wavefront of the workgroup to get here; the others exit. A wavefront's LDS operations are performed in order
+    // and the count is an acquire-release LDS atomic, so the last one reads every other's partial sums, shared rows,
+    // weights and verdict (a flag word: whether every wait of the call ended).
     if (!ok) lds_bad[1] = 1u;
-    __syncthreads();
+    __asm__ volatile("" ::"v"(touched));  // the prefetch loads count as used, so they are kept
+    uint32_t prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(&lds_bad[2], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(prev) != kFusedWaves - 1) return;
     const bool all_ok = lds_bad[1] == 0u;
-    if (owner && threadIdx.x < kOwnRows) {
-        const int r = threadIdx.x;
+    if (owner && lane < kOwnRows) {
+        const int r = lane;
         // every weight and partial read before the chain (a loop over kk waited out one LDS read per term)
         float wv[kFusedMaxK], pv[kFusedMaxK];
 #pragma unroll
@@ -822,11 +827,9 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         if (a.residual) acc = __fadd_rn(a.x[kOwnRows * b + r], acc);
         a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
     }
-    if (!all_ok && threadIdx.x == 0)  // a vector atomic, visible to the host's status query
+    if (!all_ok && lane == 0)  // a vector atomic, visible to the host's status query
         __hip_atomic_fetch_or(a.sync + kStatusWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __asm__ volatile("" ::"v"(touched));  // the prefetch loads count as used, so they are kept
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void k_zero_words(uint32_t* p, int n) {
