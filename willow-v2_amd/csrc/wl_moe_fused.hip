@@ -280,6 +280,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
     __shared__ float lds_wsel[kFusedMaxK];
     __shared__ float lds_sh[kOwnRows];
     __shared__ float lds_p[kFusedMaxK * kOwnRows];
+    __shared__ __attribute__((aligned(16))) float lds_res[kOwnRows];  // with NORM: the owner rows' x, for the residual
     __shared__ __attribute__((aligned(16))) uint64_t lds_cand[kFusedMaxE];
     __shared__ int lds_pick[kFusedMaxK];
     __shared__ uint32_t lds_bad[3];  // a wait gave up: the routing gather's, the call's; wavefronts done
@@ -341,6 +342,9 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), nw = xv, gw = xv;
         if (mine) {
             xv = reinterpret_cast<const float4*>(a.x)[threadIdx.x];
+            // the owner rows' x for the residual (LDS holds the normalized x), so the final sum reads it from LDS
+            if (b < H / kOwnRows && (static_cast<int>(threadIdx.x) >> 1) == b)
+                reinterpret_cast<float4*>(lds_res)[threadIdx.x & 1] = xv;
             if (a.norm_w) nw = reinterpret_cast<const float4*>(a.norm_w)[threadIdx.x];
             if (guess && a.guess_norm_w) gw = reinterpret_cast<const float4*>(a.guess_norm_w)[threadIdx.x];
             reinterpret_cast<float4*>(lds_xn)[x_slot(threadIdx.x)] = xv;
@@ -824,7 +828,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_moe_decode(FusedArgs a) {
         for (int s = 0; s < kFusedMaxK; s++)
             if (s < kk) acc = s == 0 ? wv[s] * pv[s] : acc + wv[s] * pv[s];
         if (shared) acc = acc + sgv * lds_sh[r];
-        if (a.residual) acc = __fadd_rn(a.x[kOwnRows * b + r], acc);
+        if (a.residual) acc = __fadd_rn(NORM ? lds_res[r] : a.x[kOwnRows * b + r], acc);
         a.y[kOwnRows * b + r] = all_ok ? acc : __builtin_nanf("");
     }
     if (!all_ok && lane == 0)  // a vector atomic, visible to the host's status query
